@@ -1,0 +1,291 @@
+"""Benchmark of the MI355X FP8-E4M3 128x128 block-dequant matmul.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--pool P] [--no-prefill]
+                    [--no-sweep] [--no-cpu] [--eager]
+
+One step = one pass of the decode hot path over one layer at M=1 token: the
+five projections 5120->6144 (qkv), 4096->5120 (o_proj), 5120->17408 (gate),
+5120->17408 (up), 17408->5120 (down), each one launch of the decode GEMV
+kernel, with weights and activations resident in HBM before timing starts.
+Steps rotate over a pool of P distinct layer copies (default 8 x 320 MB =
+2.56 GB) so the 256 MB Infinity Cache and the L2 cannot serve repeats.  The
+P copies are one generated layer with per-row sign patterns flipped
+(code ^ 0x80 on a pseudo-random half of the rows), so every copy is distinct
+data of the same distribution.
+
+value = algorithmic bytes of K steps / elapsed seconds (HIP events on the
+launch stream, launches replayed from a HIP graph), in GB/s.  Algorithmic
+bytes per matmul = N*K (e4m3) + 4*ceil(N/128)*ceil(K/128) (fp32 scales) +
+4*M*K (x) + 4*M*N (y).
+
+Also reported: the M=2/4/8 decode sweep, the M=512 prefill GEMM (TFLOP/s
+vs the bf16 dense MFMA peak), and the reference's own CPU path (AVX2 +
+OpenMP, oracle/_ref) timed on this host's cores on one layer at M=1.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qwen38-in-c_amd")
+sys.path.insert(0, PKG)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+METRIC = "M=1 FP8 GEMV HBM GB/s (% peak); M=512 prefill GEMM TFLOP/s (% MFMA peak)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def row_sign_mask(n: int, variant: int):
+    import numpy as np
+    r = np.arange(n, dtype=np.uint64)
+    h = (r * np.uint64(0x9E3779B97F4A7C15) + np.uint64(variant * 0x632BE59BD9B4E019)) >> np.uint64(63)
+    return (h.astype(np.uint8) << 7)[:, None]
+
+
+def make_layer_pool(q, wl, pool: int):
+    """pool x {qkv, o_proj, gate, up, down} resident weights + host base."""
+    base = []
+    for i, (name, k, n) in enumerate(wl.DECODE_SHAPES):
+        t = time.time()
+        W, sc = wl.gen_weight(wl.SEED_BASE + 1 + 16 * i, n, k)
+        base.append((name, k, n, W, sc))
+        log(f"  generated {name} {n}x{k} in {time.time() - t:.1f}s")
+    layers = []
+    for v in range(pool):
+        ws = []
+        for name, k, n, W, sc in base:
+            Wv = W if v == 0 else (W ^ row_sign_mask(n, v))
+            ws.append(q.Weight(Wv, sc))
+        layers.append(ws)
+    return base, layers
+
+
+def time_graph(torch, fn, steps: int, warmup: int, use_graph: bool):
+    """Run fn(i) for i in range(steps) (each i = one step), timed with events
+    on the current stream.  With use_graph the steps are captured once into
+    a HIP graph and replayed."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for i in range(steps):
+                    fn(i)
+        torch.cuda.synchronize()
+        g.replay()          # one untimed replay
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / 1e3, g
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        fn(i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3, None
+
+
+def cpu_baseline(wl, base, budget_s: float = 12.0):
+    """The reference's compiled q35_mm.c (AVX2 + OpenMP), or the oracle port
+    if the reference build is absent, on one layer at M=1."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import REF_PATH, Oracle, RefMM
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    if RefMM.available():
+        impl, kind = RefMM(), "reference"
+        run = impl.mm
+    else:
+        impl, kind = Oracle(), "port"
+        run = impl.mm
+    xs = [wl.gen_act(7 + i, 1, k)[0] for i, (_, k, _, _, _) in enumerate(base)]
+    layer_bytes = sum(wl.algorithmic_bytes(1, k, n) for _, k, n, _, _ in base)
+    for (name, k, n, W, sc), x in zip(base, xs):   # warm: page in, spin up threads
+        run(W, sc, x)
+    times = []
+    t_end = time.time() + budget_s
+    while time.time() < t_end or len(times) < 3:
+        t = time.perf_counter()
+        for (name, k, n, W, sc), x in zip(base, xs):
+            run(W, sc, x)
+        times.append(time.perf_counter() - t)
+        if len(times) >= 200:
+            break
+    med = float(np.median(times))
+    cpu = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(layer_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{len(times)} passes of one layer's 5 projections at M=1 "
+                      f"({layer_bytes / 1e6:.1f} MB), median {med * 1e3:.2f} ms/pass; "
+                      f"{'oracle/_ref q35_mm.c' if kind == 'reference' else 'oracle port'}, "
+                      f"OMP_NUM_THREADS={threads}, host CPU: {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--pool", type=int, default=8)
+    ap.add_argument("--eager", action="store_true", help="launch steps eagerly instead of from a HIP graph")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the FP8 matmul is sharded by rows across GPUs only in design; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import q35mm as q
+    import workload as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    steps = max(args.pool, (args.steps + args.pool - 1) // args.pool * args.pool)
+    t = time.time()
+    base, layers = make_layer_pool(q, wl, args.pool)
+    log(f"pool of {args.pool} layers resident ({sum(w.nbytes for w in layers[0]) * args.pool / 1e9:.2f} GB) "
+        f"in {time.time() - t:.1f}s")
+
+    def decode_step_fn(m: int):
+        xs = [torch.from_numpy(wl.gen_act(100 + i, m, k)).to(dev) for i, (_, k, _, _, _) in enumerate(base)]
+        ys = [[torch.empty((m, n), dtype=torch.float32, device=dev) for (_, _, n, _, _) in base]
+              for _ in range(args.pool)]
+
+        def fn(i):
+            li = i % args.pool
+            for j, w in enumerate(layers[li]):
+                q.gemv(w, xs[j], ys[li][j], m=m)
+        return fn, xs, ys
+
+    step_bytes = {m: sum(wl.algorithmic_bytes(m, k, n) for _, k, n, _, _ in base) for m in (1, 2, 4, 8)}
+
+    # ---- headline: M = 1 ----
+    fn, xs, ys = decode_step_fn(1)
+    el, g = time_graph(torch, fn, steps, args.warmup, not args.eager)
+    value = step_bytes[1] * steps / el / 1e9
+    ms_per_step = el / steps * 1e3
+    # the graph's outputs must equal an eager run of the same step
+    if g is not None:
+        ref_out = [y.clone() for y in ys[(steps - 1) % args.pool]]
+        fn(steps - 1)
+        torch.cuda.synchronize()
+        for a, b in zip(ref_out, ys[(steps - 1) % args.pool]):
+            assert torch.equal(a, b), "graph replay differs from eager launch"
+    log(f"M=1: {value:.1f} GB/s, {ms_per_step * 1e3:.1f} us/step ({'graph' if g is not None else 'eager'})")
+    n_launch = steps * len(base)
+    roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_fp8_kernel", "launches": n_launch,
+            "avg_launch_us": round(el / n_launch * 1e6, 3),
+            "bytes_per_launch": step_bytes[1] // len(base)}
+    del g
+
+    # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----
+    sweep = {}
+    if not args.no_sweep:
+        for m in (1, 2, 4, 8):
+            fn_m, xs_m, ys_m = decode_step_fn(m)
+            per_shape = {}
+            for j, (name, k, n, _, _) in enumerate(base):
+                def one(i, j=j):
+                    li = i % args.pool
+                    q.gemv(layers[li][j], xs_m[j], ys_m[li][j], m=m)
+                el_j, gj = time_graph(torch, one, steps, 2, not args.eager)
+                per_shape[name] = round(wl.algorithmic_bytes(m, k, n) * steps / el_j / 1e9, 1)
+                del gj
+            el_m, gm = time_graph(torch, fn_m, steps, 2, not args.eager)
+            sweep[f"M{m}"] = {"layer_GBps": round(step_bytes[m] * steps / el_m / 1e9, 1),
+                              "us_per_layer": round(el_m / steps * 1e6, 2), "per_shape_GBps": per_shape}
+            del gm
+            log(f"M={m}: {sweep[f'M{m}']}")
+
+    # ---- prefill GEMM at M = 512 ----
+    prefill = None
+    if not args.no_prefill:
+        prefill = {}
+        for i, (name, k, n) in enumerate(wl.PREFILL_SHAPES):
+            W, sc = wl.gen_weight(wl.SEED_BASE + 2 + 32 * i, n, k)
+            w = q.Weight(W, sc)
+            del W
+            X = torch.from_numpy(wl.gen_act(wl.SEED_BASE + 3 + i, 512, k, bf16=True)).to(dev)
+            Y = torch.empty((512, n), dtype=torch.float32, device=dev)
+
+            def call(_i, w=w, X=X, Y=Y):
+                q.gemm(w, X, Y)
+            el_p, gp = time_graph(torch, call, args.prefill_reps, 2, not args.eager)
+            tf = wl.flops(512, k, n) * args.prefill_reps / el_p / 1e12
+            prefill[name] = {"m": 512, "k": k, "n": n, "TFLOPs": round(tf, 1),
+                             "us": round(el_p / args.prefill_reps * 1e6, 1)}
+            log(f"prefill {name}: {tf:.1f} TFLOP/s")
+            del gp
+            w.free()
+        tot_flops = sum(wl.flops(512, k, n) for _, k, n in wl.PREFILL_SHAPES)
+        tot_us = sum(v["us"] for v in prefill.values())
+        tf_all = tot_flops / (tot_us * 1e-6) / 1e12
+        prefill["total"] = {"TFLOPs": round(tf_all, 1), "frac_of_bf16_peak": round(tf_all / BF16_PEAK_TFLOPS, 4),
+                            "note": "includes the fp32->bf16 activation prepass kernel of each call"}
+
+    cpu = None if args.no_cpu else cpu_baseline(wl, base)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 weights x fp32 activations, fp32 accumulation",
+        "data": "synthetic (seeded N(0,0.02) weights quantized per 128x128 block, N(0,1) activations)",
+        "config": {"workload": "decode GEMV, M=1, one layer's projections 5120->6144, 4096->5120, "
+                               "5120->17408 x2, 17408->5120 per step",
+                   "m": 1, "pool_layers": args.pool, "bytes_per_step": step_bytes[1],
+                   "launch": "hip graph" if not args.eager else "eager"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "decode_sweep": sweep or None,
+        "prefill": prefill,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

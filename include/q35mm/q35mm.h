@@ -1,0 +1,106 @@
+/*
+ * q35mm.h -- additive device-side API of libq35mm.so (no counterpart in the
+ * reference; the reference's q35_mm_* calls take host pointers only).
+ *
+ * It exposes what the drop-in entry points of q35/q35_mm.h do internally,
+ * for callers that keep activations in HBM and chain launches on their own
+ * stream (the benchmark, tests, and a device-resident model forward):
+ *
+ *   - weight residency: upload e4m3 codes + bf16 block scales once; the
+ *     library keeps them in HBM in a tiled, zero-padded layout with fp32
+ *     scales (see the layout notes in the implementation);
+ *   - matmuls on device pointers, asynchronous on a caller stream;
+ *   - bit-exact dequantisation to fp32 (e4m3 -> fp32, times the fp32 scale);
+ *   - explicit release of resident copies the drop-in path created.
+ *
+ * All functions return 0 on success and a negative Q35MM_E* code on failure;
+ * q35mm_last_error() describes the last failure of the calling thread.
+ * Streams are hipStream_t passed as void* (NULL = the library's own stream).
+ *
+ * Concurrency: the library keeps one split-K workspace per device.  Calls
+ * whose kernels may overlap on the GPU (different streams without ordering)
+ * race on it; serialise them on one stream.
+ */
+#ifndef Q35MM_H
+#define Q35MM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    Q35MM_OK = 0,
+    Q35MM_EINVAL = -1,    /* bad argument (null pointer, size out of range) */
+    Q35MM_EHIP = -2,      /* a HIP runtime call failed */
+    Q35MM_ENOMEM = -3,    /* device or host allocation failed */
+    Q35MM_ENODEV = -4     /* no usable gfx950 device */
+};
+
+typedef struct q35mm_weight q35mm_weight;
+
+/* Selects and initialises the device (default: HIP device 0, or the
+ * Q35MM_DEVICE environment variable).  Called implicitly by every entry
+ * point that needs the GPU. */
+int q35mm_init(int device);
+
+/* Uploads W [rows][cols] e4m3 and scale_bf16 [ceil(rows/128)][ceil(cols/128)]
+ * to HBM.  The host buffers may be freed afterwards. */
+int q35mm_weight_create(const uint8_t *W, const uint16_t *scale_bf16,
+                        uint32_t rows, uint32_t cols, q35mm_weight **out);
+/* Same, with fp32 block scales (any finite value; not expressible through
+ * the reference ABI). */
+int q35mm_weight_create_f32scale(const uint8_t *W, const float *scale_f32,
+                                 uint32_t rows, uint32_t cols,
+                                 q35mm_weight **out);
+void q35mm_weight_destroy(q35mm_weight *w);
+int q35mm_weight_shape(const q35mm_weight *w, uint32_t *rows, uint32_t *cols);
+/* Bytes of HBM held by the resident copy (codes + scales, padded). */
+size_t q35mm_weight_bytes(const q35mm_weight *w);
+
+/* Y[t][r] for t < m, X [m][cols] fp32, Y [m][rows] fp32, device pointers.
+ * Dispatch by m: m <= 8 -> decode GEMV; 8 < m < Q35MM_GEMM_MIN_M -> decode
+ * GEMV over groups of 8 tokens; m >= Q35MM_GEMM_MIN_M -> bf16 MFMA GEMM. */
+int q35mm_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
+                 void *stream);
+/* Decode GEMV for any m (groups of 8 tokens), fp32-accurate. */
+int q35mm_gemv(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
+               void *stream);
+/* Prefill GEMM for any m: activations rounded to bf16, bf16 MFMA with fp32
+ * accumulation, fp32 block scale applied per 128-wide K step. */
+int q35mm_gemm(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
+               void *stream);
+/* Up to four weights sharing cols and X, one launch (rows may differ);
+ * dY[s] is [m][rows_s].  Same results as q35mm_matmul per segment. */
+int q35mm_matmul_multi(const q35mm_weight *const *w, uint32_t nseg, uint32_t m,
+                       const float *dX, float *const *dY, void *stream);
+
+/* out [rows][cols] fp32 = e4m3(W) * scale, bit-exact. */
+int q35mm_dequant_f32(const q35mm_weight *w, float *dOut, void *stream);
+/* out [rows][cols] bf16 bits = e4m3(W) unscaled: the exact conversion the
+ * matrix-core kernels feed to MFMA. */
+int q35mm_decode_bf16(const q35mm_weight *w, uint16_t *dOut, void *stream);
+
+/* BF16 weights for q35_mm_bf16 on device pointers: W [rows][cols] bf16. */
+int q35mm_bf16_gemv(const uint16_t *dW, uint32_t rows, uint32_t cols,
+                    const float *dx, float *dy, void *stream);
+
+/* Drop the resident copy that the q35_mm_* entry points made for host
+ * pointer W (no-op if none).  q35mm_release_all drops every such copy. */
+void q35mm_release(const void *W);
+void q35mm_release_all(void);
+/* Frees every device resource of the library. */
+void q35mm_shutdown(void);
+
+const char *q35mm_last_error(void);
+
+/* Number of resident copies the drop-in entry points currently hold. */
+size_t q35mm_resident_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

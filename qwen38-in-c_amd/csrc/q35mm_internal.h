@@ -1,0 +1,103 @@
+// q35mm_internal.h -- interfaces between the host runtime (runtime.cpp) and
+// the kernel translation units.  Not installed; no C ABI here.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace q35mm {
+
+// Geometry of the lane-order tile layout (described in q35mm_device.h).
+constexpr uint32_t kBlock = 128;         // scale block edge
+constexpr uint32_t kSubRows = 32;        // rows per MFMA sub-tile
+constexpr uint32_t kChunkBytes = 1024;   // one wavefront load
+constexpr uint32_t kSubBytes = 4096;     // 32 rows x 128 columns
+constexpr uint32_t kBlockBytes = 16384;  // 128 x 128
+
+// A resident FP8 weight: lane-order tiled codes + fp32 block scales.
+struct Weight {
+    uint8_t *codes = nullptr;   // NB*128 x KB*128 bytes, layout in q35mm_device.h
+    float *scale = nullptr;     // [NB][KB] fp32 (padded blocks are 0)
+    uint32_t rows = 0, cols = 0;
+    uint32_t nb = 0, kb = 0;    // ceil(rows/128), ceil(cols/128)
+};
+
+// ---- decode GEMV (m <= 8 tokens) -------------------------------------
+constexpr uint32_t kGemvMaxM = 8;
+constexpr uint32_t kGemvMaxSliceKb = 8;   // bounds the LDS activation stage
+constexpr uint32_t kGemvThreads = 256;    // 4 wavefronts = one 128-row group
+
+struct GemvSeg {
+    const uint8_t *codes;
+    const float *scale;
+    float *y;            // token-major [m][ldy]
+    uint32_t rows;
+    uint32_t ldy;
+    uint32_t ngroups;    // = NB
+    uint32_t nslices;    // split-K factor (depends on NB, KB only)
+    uint32_t cta_begin;  // first workgroup of this segment
+    uint32_t ws_off;     // float offset of this segment's partials
+    uint32_t cnt_off;    // offset of this segment's arrival counters
+    uint32_t pad_;
+};
+
+struct GemvParams {
+    GemvSeg seg[4];
+    const float *x;      // [m][ldx] fp32
+    float *ws;           // split-K partials
+    uint32_t *cnt;       // arrival counters, zero between launches
+    uint32_t ldx;
+    uint32_t m;
+    uint32_t k;          // valid columns
+    uint32_t kb;         // KB
+    uint32_t nseg;
+    uint32_t pad_;
+};
+
+// Split-K factor for an NB x KB weight; independent of m so that a batch
+// call returns exactly the bits of m single calls.
+uint32_t gemv_slices(uint32_t nb, uint32_t kb);
+hipError_t launch_gemv(const GemvParams &p, uint32_t grid, uint32_t max_slice_kb,
+                       hipStream_t stream);
+
+// ---- prefill GEMM (bf16 MFMA) ----------------------------------------
+constexpr uint32_t kGemmTile = 128;       // BM = BN = 128
+
+struct GemmParams {
+    const uint16_t *xb;  // lane-order bf16 activations, mtiles*128 rows
+    const uint8_t *codes;
+    const float *scale;
+    float *y;            // token-major [m][ldy]
+    float *ws;
+    uint32_t *cnt;
+    uint32_t m;
+    uint32_t rows;
+    uint32_t ldy;
+    uint32_t kb;
+    uint32_t mtiles;
+    uint32_t ntiles;
+    uint32_t nslices;
+    uint32_t pad_;
+};
+
+uint32_t gemm_slices(uint32_t mtiles, uint32_t ntiles, uint32_t kb);
+// X [m][ldx] fp32 -> lane-order bf16 [mtiles*128 rows][kb*128 cols].
+hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
+                              uint32_t mtiles, uint32_t kb, uint16_t *xb,
+                              hipStream_t stream);
+hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+
+// ---- residency / conversions -----------------------------------------
+// Row-major raw codes (device) -> lane-order tiles (device).
+hipError_t launch_repack(const uint8_t *raw, uint32_t rows, uint32_t cols,
+                         uint32_t nb, uint32_t kb, uint8_t *tiled,
+                         hipStream_t stream);
+hipError_t launch_dequant_f32(const Weight &w, float *out, hipStream_t stream);
+hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream);
+
+// ---- BF16 matvec (q35_mm_bf16) ---------------------------------------
+hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols,
+                            const float *x, float *y, hipStream_t stream);
+
+}  // namespace q35mm

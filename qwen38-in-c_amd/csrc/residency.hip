@@ -1,0 +1,178 @@
+// residency.hip -- weight residency kernels: repack row-major e4m3 codes
+// into the lane-order tile layout (q35mm_device.h), bit-exact dequant to
+// fp32, and the e4m3 -> bf16 conversion the matrix-core kernels use.
+//
+// The reference binds the checkpoint's e4m3 bytes and bf16 scales zero-copy
+// from a file mapping (qwen35-c/src/q35_model.c:253-273) and dequantises
+// inside the matmul loop (qwen35-c/src/q35_mm.c:99,110-111,120); here the
+// codes are uploaded once and repacked on the device.
+#include "q35mm_device.h"
+#include "q35mm_internal.h"
+
+namespace q35mm {
+
+namespace {
+
+// Decompose a 16-byte unit index of the tiled layout.
+struct TileCoord {
+    uint32_t row, col;   // of the unit's first byte
+};
+
+__device__ __forceinline__ TileCoord unit_coord(uint32_t u, uint32_t kb_total) {
+    const uint32_t lane = u & 63;
+    const uint32_t j = (u >> 6) & 3;
+    const uint32_t sub = (u >> 8) & 3;
+    const uint32_t blk = u >> 10;                 // nb * KB + kb
+    const uint32_t kb = blk % kb_total;
+    const uint32_t nb = blk / kb_total;
+    TileCoord c;
+    c.row = nb * kBlock + sub * kSubRows + (lane & 31);
+    c.col = kb * kBlock + j * 32 + (lane >> 5) * 16;
+    return c;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ raw, uint32_t rows,
+                                                     uint32_t cols, uint32_t kb_total, uint32_t units,
+                                                     uint8_t *__restrict__ tiled) {
+    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= units) return;
+    const TileCoord c = unit_coord(u, kb_total);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (c.row < rows) {
+        const uint8_t *src = raw + (size_t)c.row * cols + c.col;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t b = (c.col + e < cols) ? src[e] : 0u;
+            w[e >> 2] |= b << (8 * (e & 3));
+        }
+    }
+    u32x4_t o = {w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<u32x4_t *>(tiled + (size_t)u * 16) = o;
+}
+
+// out[r][c] = e4m3(W[r][c]) * scale[r/128][c/128], one rounded fp32 multiply,
+// exactly the reference's lut[b] * s (qwen35-c/src/q35_mm.c:110-111,120).
+__global__ __launch_bounds__(256) void dequant_f32_kernel(const uint8_t *__restrict__ tiled,
+                                                          const float *__restrict__ scale,
+                                                          uint32_t rows, uint32_t cols,
+                                                          uint32_t kb_total, uint32_t units,
+                                                          float *__restrict__ out) {
+    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= units) return;
+    const TileCoord c = unit_coord(u, kb_total);
+    if (c.row >= rows || c.col >= cols) return;
+    const u32x4_t q = *reinterpret_cast<const u32x4_t *>(tiled + (size_t)u * 16);
+    const float s = scale[(size_t)(c.row / kBlock) * kb_total + c.col / kBlock];
+    float v[16];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const f32x2_t lo = e4m3x2_to_f32<false>(q[d]);
+        const f32x2_t hi = e4m3x2_to_f32<true>(q[d]);
+        v[4 * d + 0] = lo.x * s;
+        v[4 * d + 1] = lo.y * s;
+        v[4 * d + 2] = hi.x * s;
+        v[4 * d + 3] = hi.y * s;
+    }
+    float *dst = out + (size_t)c.row * cols + c.col;
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        if (c.col + e < cols) dst[e] = v[e];
+}
+
+// out[r][c] = bf16 bits of e4m3(W[r][c]), unscaled: the operand conversion
+// of the GEMV and GEMM kernels (e4m3x8_to_bf16x8).
+__global__ __launch_bounds__(256) void decode_bf16_kernel(const uint8_t *__restrict__ tiled,
+                                                          uint32_t rows, uint32_t cols,
+                                                          uint32_t kb_total, uint32_t units,
+                                                          uint16_t *__restrict__ out) {
+    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= units) return;
+    const TileCoord c = unit_coord(u, kb_total);
+    if (c.row >= rows || c.col >= cols) return;
+    const u32x4_t q = *reinterpret_cast<const u32x4_t *>(tiled + (size_t)u * 16);
+    const bf16x8_t lo = e4m3x8_to_bf16x8(q[0], q[1]);
+    const bf16x8_t hi = e4m3x8_to_bf16x8(q[2], q[3]);
+    const u32x4_t l4 = __builtin_bit_cast(u32x4_t, lo);
+    const u32x4_t h4 = __builtin_bit_cast(u32x4_t, hi);
+    uint16_t v[16];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        v[2 * d] = (uint16_t)(l4[d] & 0xFFFFu);
+        v[2 * d + 1] = (uint16_t)(l4[d] >> 16);
+        v[8 + 2 * d] = (uint16_t)(h4[d] & 0xFFFFu);
+        v[8 + 2 * d + 1] = (uint16_t)(h4[d] >> 16);
+    }
+    uint16_t *dst = out + (size_t)c.row * cols + c.col;
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        if (c.col + e < cols) dst[e] = v[e];
+}
+
+static uint32_t tile_units(uint32_t nb, uint32_t kb) { return nb * kb * (kBlockBytes / 16); }
+
+hipError_t launch_repack(const uint8_t *raw, uint32_t rows, uint32_t cols, uint32_t nb, uint32_t kb,
+                         uint8_t *tiled, hipStream_t stream) {
+    const uint32_t units = tile_units(nb, kb);
+    hipLaunchKernelGGL(repack_kernel, dim3((units + 255) / 256), dim3(256), 0, stream,
+                       raw, rows, cols, kb, units, tiled);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_f32(const Weight &w, float *out, hipStream_t stream) {
+    const uint32_t units = tile_units(w.nb, w.kb);
+    hipLaunchKernelGGL(dequant_f32_kernel, dim3((units + 255) / 256), dim3(256), 0, stream,
+                       w.codes, w.scale, w.rows, w.cols, w.kb, units, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream) {
+    const uint32_t units = tile_units(w.nb, w.kb);
+    hipLaunchKernelGGL(decode_bf16_kernel, dim3((units + 255) / 256), dim3(256), 0, stream,
+                       w.codes, w.rows, w.cols, w.kb, units, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------
+// BF16 matvec y[r] = sum_c bf16(W[r][c]) * x[c] (qwen35-c/src/q35_mm.c:211-246),
+// fp32 accumulation.  One wavefront per row; each lane streams 16-byte
+// loads (8 bf16) strided by 1 KiB and the wavefront reduces with a
+// butterfly of cross-lane adds.
+// ---------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bf16_gemv_kernel(const uint16_t *__restrict__ w, uint32_t rows,
+                                                        uint32_t cols, const float *__restrict__ x,
+                                                        float *__restrict__ y) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint16_t *wr = w + (size_t)row * cols;
+    float acc = 0.0f;
+    const bool aligned = ((cols & 7u) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15u) == 0);
+    uint32_t c = lane * 8;
+    if (aligned) {
+        for (; c + 8 <= cols; c += 512) {
+            const u32x4_t q = *reinterpret_cast<const u32x4_t *>(wr + c);
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                acc = __builtin_fmaf(bits_f32(q[d] << 16), x[c + 2 * d], acc);
+                acc = __builtin_fmaf(bits_f32(q[d] & 0xFFFF0000u), x[c + 2 * d + 1], acc);
+            }
+        }
+    } else {
+        for (; c < cols; c += 512)
+            for (uint32_t e = 0; e < 8 && c + e < cols; e++)
+                acc = __builtin_fmaf(bits_f32((uint32_t)wr[c + e] << 16), x[c + e], acc);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) y[row] = acc;
+}
+
+hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols, const float *x, float *y,
+                            hipStream_t stream) {
+    hipLaunchKernelGGL(bf16_gemv_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, w, rows, cols, x, y);
+    return hipGetLastError();
+}
+
+}  // namespace q35mm

@@ -1,0 +1,762 @@
+// runtime.cpp -- host side of libq35mm.so: device state, weight residency,
+// kernel dispatch, and the two C ABIs (include/q35/q35_mm.h, the drop-in for
+// qwen35-c/include/q35/q35_mm.h; include/q35mm/q35mm.h, the device API).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "q35/q35_mm.h"
+#include "q35mm/q35mm.h"
+#include "q35mm_internal.h"
+
+#define Q35MM_API extern "C" __attribute__((visibility("default")))
+
+using namespace q35mm;
+
+struct q35mm_weight {
+    Weight w;
+    size_t bytes = 0;
+};
+
+namespace {
+
+thread_local std::string t_last_error;
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_last_error = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return set_error(Q35MM_EHIP, "%s failed: %s (%s:%d)", #expr,                  \
+                             hipGetErrorString(e_), __FILE__, __LINE__);                   \
+    } while (0)
+
+[[noreturn]] void die(const char *where) {
+    fprintf(stderr, "libq35mm: %s: %s\n", where, t_last_error.c_str());
+    fflush(stderr);
+    abort();
+}
+
+uint32_t env_u32(const char *name, uint32_t dflt) {
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    return (uint32_t)strtoul(v, nullptr, 10);
+}
+
+// ---------------------------------------------------------------------
+// Device state
+// ---------------------------------------------------------------------
+struct DevBuf {
+    void *ptr = nullptr;
+    size_t cap = 0;
+};
+
+struct Device {
+    int id = -1;
+    hipStream_t stream = nullptr;
+    DevBuf ws;        // split-K partials (float)
+    DevBuf cnt;       // arrival counters (uint32, zero between launches)
+    DevBuf xb;        // bf16 lane-order activations for the GEMM
+    DevBuf dx, dy;    // activation staging for the host-pointer ABI
+    void *pin = nullptr;   // pinned host staging
+    size_t pin_cap = 0;
+    uint32_t gemm_min_m = 64;
+    bool trust_pointers = false;
+};
+
+std::recursive_mutex g_mu;
+Device g_dev;
+
+int ensure_device() {
+    if (g_dev.id >= 0) return Q35MM_OK;
+    int dev = (int)env_u32("Q35MM_DEVICE", 0);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return set_error(Q35MM_ENODEV, "no HIP device visible");
+    if (dev >= n) return set_error(Q35MM_ENODEV, "Q35MM_DEVICE=%d but %d devices", dev, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(Q35MM_ENODEV, "device %d is %s; libq35mm is built for gfx950 only", dev,
+                         prop.gcnArchName);
+    HIP_TRY(hipSetDevice(dev));
+    HIP_TRY(hipStreamCreateWithFlags(&g_dev.stream, hipStreamNonBlocking));
+    g_dev.id = dev;
+    g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
+    g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
+    return Q35MM_OK;
+}
+
+hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g_dev.stream; }
+
+// Grows a device buffer; waits for the device first because kernels queued
+// on any stream may still use the old allocation.
+int grow(DevBuf &b, size_t bytes, bool zero) {
+    if (b.cap >= bytes) return Q35MM_OK;
+    size_t cap = std::max(bytes, b.cap * 2);
+    cap = (cap + 4095) & ~(size_t)4095;
+    HIP_TRY(hipDeviceSynchronize());
+    if (b.ptr) HIP_TRY(hipFree(b.ptr));
+    b.ptr = nullptr;
+    b.cap = 0;
+    if (hipMalloc(&b.ptr, cap) != hipSuccess) {
+        b.ptr = nullptr;
+        return set_error(Q35MM_ENOMEM, "hipMalloc(%zu) failed", cap);
+    }
+    if (zero) HIP_TRY(hipMemset(b.ptr, 0, cap));
+    b.cap = cap;
+    return Q35MM_OK;
+}
+
+int grow_pinned(size_t bytes) {
+    if (g_dev.pin_cap >= bytes) return Q35MM_OK;
+    size_t cap = std::max(bytes, g_dev.pin_cap * 2);
+    cap = (cap + 4095) & ~(size_t)4095;
+    if (g_dev.pin) HIP_TRY(hipHostFree(g_dev.pin));
+    g_dev.pin = nullptr;
+    g_dev.pin_cap = 0;
+    if (hipHostMalloc(&g_dev.pin, cap, hipHostMallocDefault) != hipSuccess) {
+        g_dev.pin = nullptr;
+        return set_error(Q35MM_ENOMEM, "hipHostMalloc(%zu) failed", cap);
+    }
+    g_dev.pin_cap = cap;
+    return Q35MM_OK;
+}
+
+// ---------------------------------------------------------------------
+// Weight upload
+// ---------------------------------------------------------------------
+int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t rows, uint32_t cols,
+                  q35mm_weight **out) {
+    if (!W || !scale_f32_rowmajor || !out) return set_error(Q35MM_EINVAL, "null argument");
+    if (rows == 0 || cols == 0) return set_error(Q35MM_EINVAL, "empty weight %ux%u", rows, cols);
+    int rc = ensure_device();
+    if (rc) return rc;
+    const uint32_t nb = (rows + 127) / 128, kb = (cols + 127) / 128;
+    auto *h = new q35mm_weight();
+    h->w.rows = rows;
+    h->w.cols = cols;
+    h->w.nb = nb;
+    h->w.kb = kb;
+    const size_t tiled_bytes = (size_t)nb * kb * kBlockBytes;
+    const size_t scale_bytes = (size_t)nb * kb * sizeof(float);
+    const size_t raw_bytes = (size_t)rows * cols;
+    uint8_t *raw = nullptr;
+    auto fail = [&](int code) {
+        if (raw) (void)hipFree(raw);
+        if (h->w.codes) (void)hipFree(h->w.codes);
+        if (h->w.scale) (void)hipFree(h->w.scale);
+        delete h;
+        return code;
+    };
+    if (hipMalloc(&h->w.codes, tiled_bytes) != hipSuccess) {
+        h->w.codes = nullptr;
+        return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for weight codes failed", tiled_bytes));
+    }
+    if (hipMalloc(&h->w.scale, scale_bytes) != hipSuccess) {
+        h->w.scale = nullptr;
+        return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for scales failed", scale_bytes));
+    }
+    if (hipMalloc(&raw, raw_bytes) != hipSuccess) {
+        raw = nullptr;
+        return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for staging failed", raw_bytes));
+    }
+    hipStream_t st = g_dev.stream;
+    if (hipMemcpyAsync(raw, W, raw_bytes, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(h->w.scale, scale_f32_rowmajor, scale_bytes, hipMemcpyHostToDevice, st) !=
+            hipSuccess ||
+        launch_repack(raw, rows, cols, nb, kb, h->w.codes, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(set_error(Q35MM_EHIP, "weight upload failed: %s",
+                              hipGetErrorString(hipGetLastError())));
+    (void)hipFree(raw);
+    raw = nullptr;
+    h->bytes = tiled_bytes + scale_bytes;
+    *out = h;
+    return Q35MM_OK;
+}
+
+std::vector<float> widen_scales(const uint16_t *sc, uint32_t rows, uint32_t cols) {
+    const uint32_t nb = (rows + 127) / 128, kb = (cols + 127) / 128;
+    std::vector<float> f((size_t)nb * kb);
+    for (size_t i = 0; i < f.size(); i++) {
+        uint32_t u = (uint32_t)sc[i] << 16;
+        memcpy(&f[i], &u, 4);
+    }
+    return f;
+}
+
+// ---------------------------------------------------------------------
+// Dispatch
+// ---------------------------------------------------------------------
+int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
+                   float *const *dY, hipStream_t st) {
+    GemvParams p{};
+    const uint32_t cols = w[0]->w.cols, KB = w[0]->w.kb;
+    p.x = dX;
+    p.ldx = cols;
+    p.m = m;
+    p.k = cols;
+    p.kb = KB;
+    p.nseg = nseg;
+    uint32_t cta = 0, wsoff = 0, cntoff = 0, max_slice = 1;
+    for (uint32_t s = 0; s < nseg; s++) {
+        const Weight &ws = w[s]->w;
+        const uint32_t S = gemv_slices(ws.nb, KB);
+        GemvSeg &g = p.seg[s];
+        g.codes = ws.codes;
+        g.scale = ws.scale;
+        g.y = dY[s];
+        g.rows = ws.rows;
+        g.ldy = ws.rows;
+        g.ngroups = ws.nb;
+        g.nslices = S;
+        g.cta_begin = cta;
+        g.ws_off = wsoff;
+        g.cnt_off = cntoff;
+        cta += ws.nb * S;
+        if (S > 1) {
+            wsoff += ws.nb * S * kGemvMaxM * kBlock;
+            cntoff += ws.nb;
+        }
+        max_slice = std::max(max_slice, (KB + S - 1) / S);
+    }
+    int rc = grow(g_dev.ws, (size_t)std::max(wsoff, 1u) * sizeof(float), false);
+    if (rc) return rc;
+    rc = grow(g_dev.cnt, (size_t)std::max(cntoff, 1u) * sizeof(uint32_t), true);
+    if (rc) return rc;
+    p.ws = (float *)g_dev.ws.ptr;
+    p.cnt = (uint32_t *)g_dev.cnt.ptr;
+    HIP_TRY(launch_gemv(p, cta, max_slice, st));
+    return Q35MM_OK;
+}
+
+int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
+             float *const *dY, hipStream_t st) {
+    const uint32_t cols = w[0]->w.cols;
+    for (uint32_t t0 = 0; t0 < m; t0 += kGemvMaxM) {
+        const uint32_t mg = std::min(kGemvMaxM, m - t0);
+        float *ys[4];
+        for (uint32_t s = 0; s < nseg; s++) ys[s] = dY[s] + (size_t)t0 * w[s]->w.rows;
+        int rc = run_gemv_group(w, nseg, mg, dX + (size_t)t0 * cols, ys, st);
+        if (rc) return rc;
+    }
+    return Q35MM_OK;
+}
+
+int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hipStream_t st) {
+    const Weight &w = wt->w;
+    const uint32_t mtiles = (m + kGemmTile - 1) / kGemmTile;
+    const size_t xb_bytes = (size_t)mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
+    int rc = grow(g_dev.xb, xb_bytes, false);
+    if (rc) return rc;
+    GemmParams p{};
+    p.xb = (const uint16_t *)g_dev.xb.ptr;
+    p.codes = w.codes;
+    p.scale = w.scale;
+    p.y = dY;
+    p.m = m;
+    p.rows = w.rows;
+    p.ldy = w.rows;
+    p.kb = w.kb;
+    p.mtiles = mtiles;
+    p.ntiles = w.nb;
+    p.nslices = gemm_slices(mtiles, w.nb, w.kb);
+    const size_t tiles = (size_t)mtiles * w.nb;
+    if (p.nslices > 1) {
+        rc = grow(g_dev.ws, tiles * p.nslices * kGemmTile * kGemmTile * sizeof(float), false);
+        if (rc) return rc;
+    }
+    rc = grow(g_dev.cnt, tiles * sizeof(uint32_t), true);
+    if (rc) return rc;
+    p.ws = (float *)g_dev.ws.ptr;
+    p.cnt = (uint32_t *)g_dev.cnt.ptr;
+    HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles, w.kb, (uint16_t *)g_dev.xb.ptr, st));
+    HIP_TRY(launch_gemm(p, st));
+    return Q35MM_OK;
+}
+
+int check_weight(const q35mm_weight *w) {
+    if (!w || !w->w.codes) return set_error(Q35MM_EINVAL, "null weight handle");
+    return Q35MM_OK;
+}
+
+int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hipStream_t st) {
+    if (m == 0) return Q35MM_OK;
+    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0) return run_gemm(w, m, dX, dY, st);
+    const q35mm_weight *ws[1] = {w};
+    float *ys[1] = {dY};
+    return run_gemv(ws, 1, m, dX, ys, st);
+}
+
+// ---------------------------------------------------------------------
+// Residency registry for the host-pointer ABI
+// ---------------------------------------------------------------------
+uint64_t mix64(uint64_t h, uint64_t v) {
+    h ^= v + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+    h *= 0xff51afd7ed558ccdull;
+    return h ^ (h >> 33);
+}
+
+uint64_t hash_bytes(uint64_t h, const void *p, size_t n) {
+    const uint8_t *b = (const uint8_t *)p;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        uint64_t v;
+        memcpy(&v, b + i, 8);
+        h = mix64(h, v);
+    }
+    uint64_t tail = 0;
+    for (; i < n; i++) tail = (tail << 8) | b[i];
+    return mix64(h, tail ^ n);
+}
+
+// Sampled fingerprint of a host weight: all scales, the first and last 4 KiB
+// of the codes and 64 evenly spaced 256-byte windows.
+uint64_t fingerprint(const void *W, size_t wbytes, const void *sc, size_t scbytes) {
+    uint64_t h = hash_bytes(0x51E5ull, sc, scbytes);
+    const uint8_t *b = (const uint8_t *)W;
+    const size_t edge = std::min<size_t>(4096, wbytes);
+    h = hash_bytes(h, b, edge);
+    h = hash_bytes(h, b + wbytes - edge, edge);
+    if (wbytes > 256) {
+        for (size_t i = 0; i < 64; i++) {
+            size_t off = (wbytes - 256) / 63 * i;
+            h = hash_bytes(h, b + off, 256);
+        }
+    }
+    return h;
+}
+
+struct Resident {
+    q35mm_weight *w = nullptr;
+    const void *scale = nullptr;
+    uint32_t rows = 0, cols = 0;
+    uint64_t fp = 0;
+    bool bf16 = false;
+    uint16_t *bf16_dev = nullptr;   // q35_mm_bf16 weights (row-major, resident)
+};
+
+std::unordered_map<const void *, Resident> g_res;
+
+void drop(Resident &r) {
+    if (r.w) q35mm_weight_destroy(r.w);
+    if (r.bf16_dev) (void)hipFree(r.bf16_dev);
+    r.w = nullptr;
+    r.bf16_dev = nullptr;
+}
+
+// Resident copy for host W; uploads on first use or when the buffer behind
+// the pointer changed (shape, scale pointer or fingerprint).
+int resident_fp8(const uint8_t *W, const uint16_t *sc, uint32_t rows, uint32_t cols,
+                 q35mm_weight **out) {
+    const size_t wbytes = (size_t)rows * cols;
+    const size_t scbytes = (size_t)((rows + 127) / 128) * ((cols + 127) / 128) * 2;
+    auto it = g_res.find(W);
+    if (it != g_res.end()) {
+        Resident &r = it->second;
+        bool same = !r.bf16 && r.rows == rows && r.cols == cols && r.scale == sc;
+        if (same && !g_dev.trust_pointers) same = r.fp == fingerprint(W, wbytes, sc, scbytes);
+        if (same) {
+            *out = r.w;
+            return Q35MM_OK;
+        }
+        drop(r);
+        g_res.erase(it);
+    }
+    std::vector<float> f = widen_scales(sc, rows, cols);
+    q35mm_weight *w = nullptr;
+    int rc = weight_create(W, f.data(), rows, cols, &w);
+    if (rc) return rc;
+    Resident r;
+    r.w = w;
+    r.scale = sc;
+    r.rows = rows;
+    r.cols = cols;
+    r.fp = g_dev.trust_pointers ? 0 : fingerprint(W, wbytes, sc, scbytes);
+    g_res[W] = r;
+    *out = w;
+    return Q35MM_OK;
+}
+
+int resident_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, uint16_t **out) {
+    const size_t wbytes = (size_t)rows * cols * 2;
+    auto it = g_res.find(W);
+    if (it != g_res.end()) {
+        Resident &r = it->second;
+        bool same = r.bf16 && r.rows == rows && r.cols == cols;
+        if (same && !g_dev.trust_pointers) same = r.fp == fingerprint(W, wbytes, nullptr, 0);
+        if (same) {
+            *out = r.bf16_dev;
+            return Q35MM_OK;
+        }
+        drop(r);
+        g_res.erase(it);
+    }
+    int rc = ensure_device();
+    if (rc) return rc;
+    uint16_t *d = nullptr;
+    if (hipMalloc(&d, wbytes) != hipSuccess) return set_error(Q35MM_ENOMEM, "hipMalloc(%zu) failed", wbytes);
+    if (hipMemcpy(d, W, wbytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return set_error(Q35MM_EHIP, "bf16 weight upload failed");
+    }
+    Resident r;
+    r.bf16 = true;
+    r.bf16_dev = d;
+    r.rows = rows;
+    r.cols = cols;
+    r.fp = g_dev.trust_pointers ? 0 : fingerprint(W, wbytes, nullptr, 0);
+    g_res[W] = r;
+    *out = d;
+    return Q35MM_OK;
+}
+
+// Host-pointer round trip: X (n*cols floats) in, outputs of nseg segments
+// out.  'run' launches on g_dev.stream reading dx and writing dy[s].
+template <class Run>
+int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t *yfloats,
+                   uint32_t nseg, Run run) {
+    size_t ytotal = 0;
+    for (uint32_t s = 0; s < nseg; s++) ytotal += yfloats[s];
+    int rc = grow(g_dev.dx, xfloats * sizeof(float), false);
+    if (!rc) rc = grow(g_dev.dy, ytotal * sizeof(float), false);
+    if (!rc) rc = grow_pinned((xfloats + ytotal) * sizeof(float));
+    if (rc) return rc;
+    float *px = (float *)g_dev.pin;
+    float *py = px + xfloats;
+    hipStream_t st = g_dev.stream;
+    memcpy(px, X, xfloats * sizeof(float));
+    HIP_TRY(hipMemcpyAsync(g_dev.dx.ptr, px, xfloats * sizeof(float), hipMemcpyHostToDevice, st));
+    float *dys[4];
+    size_t off = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        dys[s] = (float *)g_dev.dy.ptr + off;
+        off += yfloats[s];
+    }
+    rc = run((const float *)g_dev.dx.ptr, dys);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    off = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        memcpy(Y[s], py + off, yfloats[s] * sizeof(float));
+        off += yfloats[s];
+    }
+    return Q35MM_OK;
+}
+
+// ---------------------------------------------------------------------
+// e4m3 decode table (host)
+// ---------------------------------------------------------------------
+float e4m3_decode(uint8_t v) {
+    const uint32_t sign = (uint32_t)(v >> 7) << 31;
+    const uint32_t e = (v >> 3) & 0xF, m = v & 7;
+    uint32_t bits;
+    if (e == 0) {
+        float f = (float)m * 0x1.0p-9f;
+        memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else if (e == 15 && m == 7) {
+        bits = sign | 0x7FC00000u;
+    } else {
+        bits = sign | ((e + 120) << 23) | (m << 20);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void fill_lut(float *lut) {
+    for (int i = 0; i < 256; i++) lut[i] = e4m3_decode((uint8_t)i);
+}
+
+__attribute__((constructor)) void lut_at_load() { fill_lut(q35_mm_fp8_lut); }
+
+}  // namespace
+
+// =====================================================================
+// Drop-in ABI (include/q35/q35_mm.h)
+// =====================================================================
+// Braced linkage block: this is the definition of the exported data symbol
+// (the single-declaration form extern "C" T x; only declares it).
+extern "C" {
+__attribute__((visibility("default"))) float q35_mm_fp8_lut[256];
+}
+
+Q35MM_API void q35_mm_init(void) {
+    static std::once_flag once;
+    std::call_once(once, [] { fill_lut(q35_mm_fp8_lut); });
+}
+
+Q35MM_API float q35_mm_e4m3_to_f32(uint8_t v) { return e4m3_decode(v); }
+
+Q35MM_API float q35_mm_bf16_to_f32(uint16_t v) {
+    uint32_t u = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+Q35MM_API const char *q35_mm_impl_fp8(void) { return "hip-gfx950"; }
+
+Q35MM_API void q35_mm_fp8_batch(const uint8_t *W, const uint16_t *scale_bf16, uint32_t rows,
+                                uint32_t cols, uint32_t n, const float *X, float *Y) {
+    if (rows == 0 || n == 0) return;
+    if (cols == 0) {
+        memset(Y, 0, (size_t)n * rows * sizeof(float));
+        return;
+    }
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    q35mm_weight *w = nullptr;
+    if (!rc) rc = resident_fp8(W, scale_bf16, rows, cols, &w);
+    if (!rc) {
+        float *ys[1] = {Y};
+        size_t yf[1] = {(size_t)n * rows};
+        rc = host_roundtrip(X, (size_t)n * cols, ys, yf, 1, [&](const float *dx, float **dy) {
+            return run_matmul(w, n, dx, dy[0], g_dev.stream);
+        });
+    }
+    if (rc) die("q35_mm_fp8_batch");
+}
+
+Q35MM_API void q35_mm_fp8(const uint8_t *W, const uint16_t *scale_bf16, uint32_t rows, uint32_t cols,
+                          const float *x, float *y) {
+    q35_mm_fp8_batch(W, scale_bf16, rows, cols, 1, x, y);
+}
+
+Q35MM_API void q35_mm_fp8_multi4(const uint8_t *W[4], const uint16_t *sc[4], uint32_t rows[4],
+                                 uint32_t cols, const float *x, float *y[4]) {
+    uint32_t idx[4], nseg = 0;
+    for (uint32_t s = 0; s < 4; s++)
+        if (rows[s]) idx[nseg++] = s;
+    if (nseg == 0) return;
+    if (cols == 0) {
+        for (uint32_t i = 0; i < nseg; i++) memset(y[idx[i]], 0, (size_t)rows[idx[i]] * sizeof(float));
+        return;
+    }
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    q35mm_weight *ws[4];
+    for (uint32_t i = 0; i < nseg && !rc; i++) rc = resident_fp8(W[idx[i]], sc[idx[i]], rows[idx[i]], cols, &ws[i]);
+    if (!rc) {
+        float *ys[4];
+        size_t yf[4];
+        for (uint32_t i = 0; i < nseg; i++) {
+            ys[i] = y[idx[i]];
+            yf[i] = rows[idx[i]];
+        }
+        rc = host_roundtrip(x, cols, ys, yf, nseg, [&](const float *dx, float **dy) {
+            return run_gemv(ws, nseg, 1, dx, dy, g_dev.stream);
+        });
+    }
+    if (rc) die("q35_mm_fp8_multi4");
+}
+
+Q35MM_API void q35_mm_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, const float *x, float *y) {
+    if (rows == 0) return;
+    if (cols == 0) {
+        memset(y, 0, (size_t)rows * sizeof(float));
+        return;
+    }
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    uint16_t *dw = nullptr;
+    if (!rc) rc = resident_bf16(W, rows, cols, &dw);
+    if (!rc) {
+        float *ys[1] = {y};
+        size_t yf[1] = {rows};
+        rc = host_roundtrip(x, cols, ys, yf, 1, [&](const float *dx, float **dy) -> int {
+            HIP_TRY(launch_bf16_gemv(dw, rows, cols, dx, dy[0], g_dev.stream));
+            return Q35MM_OK;
+        });
+    }
+    if (rc) die("q35_mm_bf16");
+}
+
+// =====================================================================
+// Device API (include/q35mm/q35mm.h)
+// =====================================================================
+Q35MM_API int q35mm_init(int device) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (device >= 0 && g_dev.id < 0) {
+        char buf[16];
+        snprintf(buf, sizeof buf, "%d", device);
+        setenv("Q35MM_DEVICE", buf, 1);
+    }
+    return ensure_device();
+}
+
+Q35MM_API int q35mm_weight_create(const uint8_t *W, const uint16_t *scale_bf16, uint32_t rows,
+                                  uint32_t cols, q35mm_weight **out) {
+    if (!W || !scale_bf16 || !out) return set_error(Q35MM_EINVAL, "null argument");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    std::vector<float> f = widen_scales(scale_bf16, rows, cols);
+    return weight_create(W, f.data(), rows, cols, out);
+}
+
+Q35MM_API int q35mm_weight_create_f32scale(const uint8_t *W, const float *scale_f32, uint32_t rows,
+                                           uint32_t cols, q35mm_weight **out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return weight_create(W, scale_f32, rows, cols, out);
+}
+
+Q35MM_API void q35mm_weight_destroy(q35mm_weight *w) {
+    if (!w) return;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    (void)hipDeviceSynchronize();
+    if (w->w.codes) (void)hipFree(w->w.codes);
+    if (w->w.scale) (void)hipFree(w->w.scale);
+    delete w;
+}
+
+Q35MM_API int q35mm_weight_shape(const q35mm_weight *w, uint32_t *rows, uint32_t *cols) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    if (rows) *rows = w->w.rows;
+    if (cols) *cols = w->w.cols;
+    return Q35MM_OK;
+}
+
+Q35MM_API size_t q35mm_weight_bytes(const q35mm_weight *w) { return w ? w->bytes : 0; }
+
+Q35MM_API int q35mm_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(w);
+    if (rc) return rc;
+    if (m && (!dX || !dY)) return set_error(Q35MM_EINVAL, "null activation pointer");
+    return run_matmul(w, m, dX, dY, pick_stream(stream));
+}
+
+Q35MM_API int q35mm_gemv(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(w);
+    if (rc) return rc;
+    if (m == 0) return Q35MM_OK;
+    if (!dX || !dY) return set_error(Q35MM_EINVAL, "null activation pointer");
+    const q35mm_weight *ws[1] = {w};
+    float *ys[1] = {dY};
+    return run_gemv(ws, 1, m, dX, ys, pick_stream(stream));
+}
+
+Q35MM_API int q35mm_gemm(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(w);
+    if (rc) return rc;
+    if (m == 0) return Q35MM_OK;
+    if (!dX || !dY) return set_error(Q35MM_EINVAL, "null activation pointer");
+    return run_gemm(w, m, dX, dY, pick_stream(stream));
+}
+
+Q35MM_API int q35mm_matmul_multi(const q35mm_weight *const *w, uint32_t nseg, uint32_t m,
+                                 const float *dX, float *const *dY, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!w || !dY || nseg == 0 || nseg > 4) return set_error(Q35MM_EINVAL, "need 1..4 segments");
+    for (uint32_t s = 0; s < nseg; s++) {
+        rc = check_weight(w[s]);
+        if (rc) return rc;
+        if (w[s]->w.cols != w[0]->w.cols) return set_error(Q35MM_EINVAL, "segments differ in cols");
+    }
+    if (m == 0) return Q35MM_OK;
+    hipStream_t st = pick_stream(stream);
+    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0) {
+        for (uint32_t s = 0; s < nseg; s++) {
+            rc = run_gemm(w[s], m, dX, dY[s], st);
+            if (rc) return rc;
+        }
+        return Q35MM_OK;
+    }
+    return run_gemv(w, nseg, m, dX, dY, st);
+}
+
+Q35MM_API int q35mm_dequant_f32(const q35mm_weight *w, float *dOut, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(w);
+    if (rc) return rc;
+    HIP_TRY(launch_dequant_f32(w->w, dOut, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_decode_bf16(const q35mm_weight *w, uint16_t *dOut, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(w);
+    if (rc) return rc;
+    HIP_TRY(launch_decode_bf16(w->w, dOut, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_bf16_gemv(const uint16_t *dW, uint32_t rows, uint32_t cols, const float *dx, float *dy,
+                              void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (rows == 0) return Q35MM_OK;
+    if (!dW || !dx || !dy) return set_error(Q35MM_EINVAL, "null pointer");
+    HIP_TRY(launch_bf16_gemv(dW, rows, cols, dx, dy, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API void q35mm_release(const void *W) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g_res.find(W);
+    if (it == g_res.end()) return;
+    drop(it->second);
+    g_res.erase(it);
+}
+
+Q35MM_API void q35mm_release_all(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    for (auto &kv : g_res) drop(kv.second);
+    g_res.clear();
+}
+
+Q35MM_API size_t q35mm_resident_count(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return g_res.size();
+}
+
+Q35MM_API void q35mm_shutdown(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    q35mm_release_all();
+    if (g_dev.id < 0) return;
+    (void)hipDeviceSynchronize();
+    for (DevBuf *b : {&g_dev.ws, &g_dev.cnt, &g_dev.xb, &g_dev.dx, &g_dev.dy}) {
+        if (b->ptr) (void)hipFree(b->ptr);
+        b->ptr = nullptr;
+        b->cap = 0;
+    }
+    if (g_dev.pin) (void)hipHostFree(g_dev.pin);
+    g_dev.pin = nullptr;
+    g_dev.pin_cap = 0;
+    if (g_dev.stream) (void)hipStreamDestroy(g_dev.stream);
+    g_dev.stream = nullptr;
+    g_dev.id = -1;
+}
+
+Q35MM_API const char *q35mm_last_error(void) { return t_last_error.c_str(); }
