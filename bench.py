@@ -46,7 +46,9 @@ def log(*a):
 def row_sign_mask(n: int, variant: int):
     import numpy as np
     r = np.arange(n, dtype=np.uint64)
-    h = (r * np.uint64(0x9E3779B97F4A7C15) + np.uint64(variant * 0x632BE59BD9B4E019)) >> np.uint64(63)
+    salt = np.uint64((variant * 0x632BE59BD9B4E019) & 0xFFFFFFFFFFFFFFFF)
+    with np.errstate(over="ignore"):
+        h = (r * np.uint64(0x9E3779B97F4A7C15) + salt) >> np.uint64(63)
     return (h.astype(np.uint8) << 7)[:, None]
 
 

@@ -15,7 +15,7 @@
  *
  * All functions return 0 on success and a negative Q35MM_E* code on failure;
  * q35mm_last_error() describes the last failure of the calling thread.
- * Streams are hipStream_t passed as void* (NULL = the library's own stream).
+ * Streams are hipStream_t passed as void*; NULL is HIP's null stream.
  *
  * Concurrency: the library keeps one split-K workspace per device.  Calls
  * whose kernels may overlap on the GPU (different streams without ordering)

@@ -4,28 +4,33 @@
 // Replaces the hot loop of qwen35-c/src/q35_mm.c:88-198 (mm_fp8_row called
 // by q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4).
 //
-// Work decomposition.  A workgroup of four wavefronts owns one 128-row group
-// (one scale row-block) and a slice of the K blocks; wavefront w owns the
-// 32-row sub-tile w.  Each wavefront streams its weights with one 16-byte
-// load per lane per 1 KiB chunk (the lane-order tile layout makes every load
-// a contiguous 1 KiB), converts e4m3 -> bf16 in registers (exact) and feeds
-// v_mfma_f32_32x32x16_bf16.
+// Arithmetic.  Weights are converted e4m3 -> bf16 in registers (exact) and
+// fed to v_mfma_f32_32x32x16_bf16.  Activations are fp32; each is split
+// exactly into three bf16 parts x = p0 + p1 + p2, and the A-operand rows are
+// m = t + 8p (token t < 8, part p < 3), so one MFMA forms the three partial
+// dot products of up to eight tokens.  Products e4m3*bf16 are exact in fp32;
+// the only rounding is fp32 accumulation.  Per 128-column K block the MFMA
+// accumulator holds the raw block dot product, which is multiplied by the
+// block's fp32 scale and added to the running sum (one fmaf per output and
+// block).
 //
-// Activations are fp32.  To keep fp32 accuracy on a bf16 matrix core, every
-// activation is split exactly into three bf16 parts x = p0 + p1 + p2; the A
-// operand rows are m = t + 8p (token t < 8, part p < 3), so one MFMA computes
-// the three partial dot products of up to eight tokens at once.  The
-// products e4m3*bf16 are exact in fp32; the only rounding is the fp32
-// accumulation.  Per 128-column K block the MFMA accumulator holds the raw
-// block dot product, which is then multiplied by the block's fp32 scale and
-// added to the running sum (one fmaf per output and block).
+// Decomposition (stream-K).  A weight is a sequence of T = NB*KB 16 KiB
+// blocks (128-row group g, K block kb) in (g, kb) order.  Its grid is a
+// fixed P workgroups (two per CU by default); workgroup c takes the
+// contiguous block range [c*T/P, (c+1)*T/P), so every CU streams the same
+// number of bytes whatever the shape.  Several weights sharing K (the
+// reference's multi4) get one grid each, concatenated into one launch.
+// Wavefront w of a workgroup owns 32-row sub-tile w of every block, streams
+// it with one 16-byte load per lane per 1 KiB chunk (the lane-order tile
+// layout makes every load a contiguous 1 KiB) and keeps a ring of
+// kGemvDepth blocks in flight across group boundaries.
 //
-// Split-K: when a slice does not cover all K blocks, each workgroup writes
-// its partial outputs to a workspace, and the last workgroup of a row group
-// to arrive (device-scope atomic ticket) adds the partials in slice order
-// and writes y.  The order is fixed, so results do not depend on timing, and
-// the slice count depends only on the weight shape, so a batch of m tokens
-// gives exactly the bits of m single-token calls.
+// A group wholly inside one range is written to y directly.  A group split
+// between ranges is finished by its last contributor to arrive: each
+// contributor publishes its partial outputs, takes a ticket, and the last
+// one adds the partials in range order.  That order is fixed by the shape,
+// so results do not depend on timing, and P depends only on the shape, so a
+// batch of m tokens gives exactly the bits of m single-token calls.
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
 
@@ -37,40 +42,69 @@ __device__ __forceinline__ u32x4_t ld16(const uint8_t *p) {
     return *reinterpret_cast<const u32x4_t *>(p);
 }
 
-// Stage the three-part bf16 split of x[t][kb0*128 .. (kb0+nkb)*128) for
-// t < m into LDS in MFMA A-operand order:
+// Activation staging.  The three-part bf16 split of the activations for the
+// workgroup's blocks goes to LDS in MFMA A-operand order.  Slot i holds K
+// block (b0 + i) mod KB:
 //   byte offset(c, q, ai, h) = (((c*2 + q) * R + ai) * 2 + h) * 16
-// where c is the slice-relative 32-column chunk, q selects the first or the
-// second MFMA of the chunk, ai = part*m + t, R = 3m, h = lane/32, and the 16
-// bytes hold columns c*32 + 16h + 8q + (0..7).
-__device__ void stage_split_x(uint8_t *lds, const float *x, uint32_t ldx, uint32_t m,
-                              uint32_t k, uint32_t kb0, uint32_t nkb) {
+// where c = i*4 + chunk, q selects the first or second MFMA of the chunk,
+// ai = part*m + t, R = 3m, h = lane/32, and the 16 bytes hold columns
+// kb*128 + chunk*32 + 16h + 8q + (0..7).
+//
+// Work item v (< m * nblk * 16) is one 8-column vector of one token.  The
+// loads of a thread's first kStagePre items are split from the rest so they
+// can be issued before the weight prologue: memory loads complete in issue
+// order, so anything issued before the weights can be waited for without
+// waiting for the weights.
+constexpr uint32_t kStagePre = 2;
+
+struct StageItem {
+    uint32_t t, kk, kg;   // token, slot-relative column, global column
+};
+
+__device__ __forceinline__ StageItem stage_item(uint32_t i, uint32_t per_t, uint32_t kb_total, uint32_t b0) {
+    StageItem it;
+    it.t = i / per_t;
+    const uint32_t v = i - it.t * per_t;
+    const uint32_t slot = v >> 4;
+    it.kk = slot * kBlock + (v & 15) * 8;
+    it.kg = ((b0 + slot) % kb_total) * kBlock + (v & 15) * 8;
+    return it;
+}
+
+// Raw loads of one item; the address is clamped into the row so the loads
+// are unconditional (no branch between them and the weight prologue).  The
+// caller zeroes columns >= k before use (stage_mask).
+__device__ __forceinline__ void stage_load(float (&xv)[8], const float *x, uint32_t ldx, uint32_t k,
+                                           const StageItem &it) {
+    const float *xp = x + (size_t)it.t * ldx;
+#pragma unroll
+    for (int e = 0; e < 8; e++) xv[e] = xp[min(it.kg + e, k - 1)];
+}
+
+__device__ __forceinline__ void stage_mask(float (&xv)[8], uint32_t k, const StageItem &it) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) xv[e] = (it.kg + e < k) ? xv[e] : 0.0f;
+}
+
+__device__ __forceinline__ void stage_store(uint8_t *lds, uint32_t m, const StageItem &it, const float (&xv)[8]) {
     const uint32_t R = 3 * m;
-    const uint32_t per_t = nkb * 16;               // 8-column vectors per token
-    const uint32_t nvec = m * per_t;
-    for (uint32_t i = threadIdx.x; i < nvec; i += blockDim.x) {
-        const uint32_t t = i / per_t;
-        const uint32_t kk = (i - t * per_t) * 8;   // slice-relative column
-        const uint32_t kg = kb0 * kBlock + kk;     // global column
-        const float *xp = x + (size_t)t * ldx + kg;
-        float v[8];
+    uint32_t p0[8], p1[8], p2[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (kg + e < k) ? xp[e] : 0.0f;
-        uint32_t p0[8], p1[8], p2[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) split3_bf16(v[e], p0[e], p1[e], p2[e]);
-        const uint32_t c = kk >> 5, h = (kk >> 4) & 1, q = (kk >> 3) & 1;
-        const uint32_t base = (c * 2 + q) * R;
-        u32x4_t w0 = {p0[0] | (p0[1] << 16), p0[2] | (p0[3] << 16),
-                      p0[4] | (p0[5] << 16), p0[6] | (p0[7] << 16)};
-        u32x4_t w1 = {p1[0] | (p1[1] << 16), p1[2] | (p1[3] << 16),
-                      p1[4] | (p1[5] << 16), p1[6] | (p1[7] << 16)};
-        u32x4_t w2 = {p2[0] | (p2[1] << 16), p2[2] | (p2[3] << 16),
-                      p2[4] | (p2[5] << 16), p2[6] | (p2[7] << 16)};
-        *reinterpret_cast<u32x4_t *>(lds + ((base + 0 * m + t) * 2 + h) * 16) = w0;
-        *reinterpret_cast<u32x4_t *>(lds + ((base + 1 * m + t) * 2 + h) * 16) = w1;
-        *reinterpret_cast<u32x4_t *>(lds + ((base + 2 * m + t) * 2 + h) * 16) = w2;
-    }
+    for (int e = 0; e < 8; e++) split3_bf16(xv[e], p0[e], p1[e], p2[e]);
+    const uint32_t c = it.kk >> 5, h = (it.kk >> 4) & 1, q = (it.kk >> 3) & 1;
+    const uint32_t base = (c * 2 + q) * R;
+    u32x4_t w0 = {p0[0] | (p0[1] << 16), p0[2] | (p0[3] << 16), p0[4] | (p0[5] << 16), p0[6] | (p0[7] << 16)};
+    u32x4_t w1 = {p1[0] | (p1[1] << 16), p1[2] | (p1[3] << 16), p1[4] | (p1[5] << 16), p1[6] | (p1[7] << 16)};
+    u32x4_t w2 = {p2[0] | (p2[1] << 16), p2[2] | (p2[3] << 16), p2[4] | (p2[5] << 16), p2[6] | (p2[7] << 16)};
+    *reinterpret_cast<u32x4_t *>(lds + ((base + 0 * m + it.t) * 2 + h) * 16) = w0;
+    *reinterpret_cast<u32x4_t *>(lds + ((base + 1 * m + it.t) * 2 + h) * 16) = w1;
+    *reinterpret_cast<u32x4_t *>(lds + ((base + 2 * m + it.t) * 2 + h) * 16) = w2;
+}
+
+// The workgroup whose range holds a given block: the largest c with
+// floor(c*T/P) <= block.
+__device__ __forceinline__ uint32_t range_of(uint64_t block, uint32_t T, uint32_t P) {
+    return (uint32_t)(((block + 1) * P + T - 1) / T) - 1;
 }
 
 }  // namespace
@@ -79,139 +113,257 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t s_ticket;
 
-    // ---- which segment / row group / K slice ----
-    const uint32_t b = blockIdx.x;
+    // ---- segment and block range of this workgroup ----
     uint32_t si = 0;
 #pragma unroll
     for (uint32_t i = 1; i < 4; i++)
-        if (i < p.nseg && b >= p.seg[i].cta_begin) si = i;
-    const GemvSeg sg = p.seg[si];
-    const uint32_t S = sg.nslices;
-    const uint32_t local = b - sg.cta_begin;
-    const uint32_t g = local / S;
-    const uint32_t s = local - g * S;
-    const uint32_t KB = p.kb;
-    const uint32_t kb0 = (s * KB) / S;
-    const uint32_t kb1 = ((s + 1) * KB) / S;
-    const uint32_t M = p.m;
-
-    stage_split_x(lds, p.x, p.ldx, M, p.k, kb0, kb1 - kb0);
-    __syncthreads();
+        if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
+    const GemvSeg &sg = p.seg[si];
+    const uint32_t c = blockIdx.x - sg.cta_begin;
+    const uint32_t KB = p.kb, M = p.m;
+    const uint32_t P = sg.nctas, T = sg.nb * KB;
+    const uint32_t b0 = (uint32_t)(((uint64_t)c * T) / P);
+    const uint32_t b1 = (uint32_t)(((uint64_t)(c + 1) * T) / P);
+    const uint32_t nblk = b1 - b0;                 // >= 1 (P <= T)
 
     // ---- per-lane roles ----
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wv = threadIdx.x >> 6;         // 32-row sub-tile
+    const uint32_t wv = threadIdx.x >> 6;          // 32-row sub-tile
     const uint32_t mrow = lane & 31, hh = lane >> 5;
     const uint32_t tt = mrow & 7, pp = mrow >> 3;  // A row = token + 8*part
     const bool a_active = (tt < M) && (pp < 3);
     const uint32_t R = 3 * M;
-    const uint32_t a_lane_off = ((pp * M + tt) * 2 + hh) * 16;
+    // A-operand address = a_base + (chunk*2 + q) * a_step.  Rows that carry
+    // no token (t >= m, or the unused rows 24..31) read a 16-byte zero slot
+    // placed after the stage, so every lane issues the same LDS read.
+    const uint32_t zero_off = nblk * 256 * R;
+    const uint32_t a_base = a_active ? ((pp * M + tt) * 2 + hh) * 16 : zero_off;
+    const uint32_t a_step = a_active ? R * 32 : 0;
+    const uint32_t lane_off = wv * kSubBytes + lane * 16;
 
-    const uint8_t *wbase = sg.codes + (size_t)g * KB * kBlockBytes + wv * kSubBytes + lane * 16;
-    const float *srow = sg.scale + (size_t)g * KB;
+    // ---- weight stream: a ring of kGemvDepth blocks in registers ----
+    // Loads are unconditional (block index clamped into the range; the few
+    // repeated tail loads hit in cache) so that the wait before each block is
+    // a static vmcnt and kGemvDepth-1 blocks stay in flight.  Each block's
+    // scale travels with it through a matching ring.
+    u32x4_t buf[kGemvDepth][4];
+    float scs[kGemvDepth];
+    const uint8_t *codes = sg.codes + lane_off;
+    const float *scale = sg.scale;
+    auto load = [&](u32x4_t (&dst)[4], float &sc, uint32_t b) {
+        const uint8_t *src = codes + (size_t)b * kBlockBytes;   // block b = g*KB + kb
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[j] = ld16(src + j * kChunkBytes);
+        sc = scale[b];
+    };
+
+    // ---- prologue: activation loads, then the first weight blocks ----
+    const uint32_t per_t = nblk * 16;
+    const uint32_t nvec = M * per_t;
+    float xpre[kStagePre][8];
+#pragma unroll
+    for (uint32_t u = 0; u < kStagePre; u++)   // index clamped: loads are unconditional
+        stage_load(xpre[u], p.x, p.ldx, p.k, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], scs[d], min(b0 + d, b1 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    // Split and stage while the weight blocks are in flight.
+#pragma unroll
+    for (uint32_t u = 0; u < kStagePre; u++) {
+        const uint32_t i = threadIdx.x + u * kGemvThreads;
+        const StageItem it = stage_item(min(i, nvec - 1), per_t, KB, b0);
+        stage_mask(xpre[u], p.k, it);
+        if (i < nvec) stage_store(lds, M, it, xpre[u]);
+    }
+    for (uint32_t i = threadIdx.x + kStagePre * kGemvThreads; i < nvec; i += kGemvThreads) {
+        const StageItem it = stage_item(i, per_t, KB, b0);
+        float xv[8];
+        stage_load(xv, p.x, p.ldx, p.k, it);
+        stage_mask(xv, p.k, it);
+        stage_store(lds, M, it, xv);
+    }
+    if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + zero_off)[threadIdx.x] = 0u;
+    __syncthreads();
 
     f32x16_t acc = {};
     const f32x16_t zero = {};
 
-    auto compute = [&](const u32x4_t (&wq)[4], uint32_t kb) {
-        const uint32_t cbase = (kb - kb0) * 4;
+    auto compute = [&](const u32x4_t (&wq)[4], float sc, uint32_t slot) {
+        const uint32_t cbase = slot * 4;
+        // All eight A-operand reads of the block first: their latency is paid
+        // once per block.
+        u32x4_t araw[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            araw[i] = *reinterpret_cast<const u32x4_t *>(lds + a_base + (cbase * 2 + i) * a_step);
+        __builtin_amdgcn_sched_barrier(0);
         f32x16_t part;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 const bf16x8_t bop = e4m3x8_to_bf16x8(wq[j][2 * q], wq[j][2 * q + 1]);
-                u32x4_t araw = {0u, 0u, 0u, 0u};
-                if (a_active)
-                    araw = *reinterpret_cast<const u32x4_t *>(
-                        lds + ((cbase + j) * 2 + q) * R * 32 + a_lane_off);
-                const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw);
+                const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
                 part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
             }
         }
-        const float sc = srow[kb];
         // Rows 24..31 of the A operand are never used (regs 12..15).
 #pragma unroll
         for (int r = 0; r < 12; r++) acc[r] = __builtin_fmaf(sc, part[r], acc[r]);
     };
 
-    // ---- stream the slice, one K block of loads ahead ----
-    u32x4_t wa[4], wb[4];
-    auto load = [&](u32x4_t (&dst)[4], uint32_t kb) {
-        const uint8_t *src = wbase + (size_t)kb * kBlockBytes;
+    // ---- finishing a group segment [gs, ge) of this range ----
+    // Only the first and the last segment of a range can be part of a split
+    // group; pend* remember split groups this workgroup arrived last at.
+    // They are reduced after the stream so the ring is not held up.
+    bool pend0 = false, pend1 = false;
+    uint32_t pg0 = 0, pg1 = 0;
+    auto flush = [&](uint32_t G, uint32_t gs, uint32_t ge, bool first) {
+        float yv[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) dst[j] = ld16(src + j * kChunkBytes);
-    };
-    load(wa, kb0);
-    for (uint32_t kb = kb0; kb < kb1; kb += 2) {
-        if (kb + 1 < kb1) load(wb, kb + 1);
-        compute(wa, kb);
-        if (kb + 1 < kb1) {
-            if (kb + 2 < kb1) load(wa, kb + 2);
-            compute(wb, kb + 1);
+        for (int r = 0; r < 4; r++) yv[r] = (acc[r] + acc[r + 4]) + acc[r + 8];
+        const uint32_t rl = wv * 32 + mrow;
+        const uint32_t row = G * kBlock + rl;
+        if (ge - gs == KB) {   // the whole group is in this range
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t t = 4 * hh + r;
+                if (t < M && row < sg.rows) sg.y[(size_t)t * sg.ldy + row] = yv[r];
+            }
+            return;
         }
-    }
-
-    // ---- combine the three parts: token t = 4*hh + r ----
-    float yv[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) yv[r] = (acc[r] + acc[r + 4]) + acc[r + 8];
-    const uint32_t row_local = wv * 32 + mrow;
-    const uint32_t row = g * kBlock + row_local;
-
-    if (S == 1) {
+        // Publish the partial with device-scope atomic stores (they reach the
+        // coherence point instead of staying dirty in this XCD's L2, so no L2
+        // writeback is needed), wait until they are complete, take a ticket.
+        const uint32_t cfirst = range_of((uint64_t)G * KB, T, P);
+        const uint32_t clast = range_of((uint64_t)G * KB + KB - 1, T, P);
+        float *slot = p.ws + sg.ws_off + ((size_t)G * sg.maxc + (c - cfirst)) * (kGemvMaxM * kBlock);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint32_t t = 4 * hh + r;
-            if (t < M && row < sg.rows) sg.y[(size_t)t * sg.ldy + row] = yv[r];
+            if (t < M)
+                __hip_atomic_store(slot + t * kBlock + rl, yv[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        return;
-    }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_ticket = __hip_atomic_fetch_add(p.cnt + sg.cnt_off + G, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_ticket == clast - cfirst) {
+            if (first) {
+                pend0 = true;
+                pg0 = G;
+            } else {
+                pend1 = true;
+                pg1 = G;
+            }
+        }
+    };
 
-    float *ws = p.ws + sg.ws_off;
+    uint32_t gcur = b0 / KB, gstart = b0;
+    bool first_seg = true;
+    for (uint32_t b = b0; b < b1; b += kGemvDepth) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t t = 4 * hh + r;
-        if (t < M) ws[(((size_t)g * S + s) * kGemvMaxM + t) * kBlock + row_local] = yv[r];
+        for (uint32_t d = 0; d < kGemvDepth; d++) {
+            const uint32_t bb = b + d;
+            constexpr uint32_t nx = kGemvDepth - 1;
+            load(buf[(d + nx) % kGemvDepth], scs[(d + nx) % kGemvDepth], min(bb + nx, b1 - 1));
+            // Keep the scheduler from sinking these loads below the math of
+            // block bb (it would, to reuse their registers).
+            __builtin_amdgcn_sched_barrier(0);
+            if (bb < b1) {
+                const uint32_t G = bb / KB;
+                if (G != gcur) {
+                    flush(gcur, gstart, bb, first_seg);
+                    first_seg = false;
+                    gcur = G;
+                    gstart = bb;
+                    acc = zero;
+                }
+                compute(buf[d], scs[d], bb - b0);
+            }
+        }
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_ticket = atomicAdd(p.cnt + sg.cnt_off + g, 1u);
-    __syncthreads();
-    if (s_ticket != S - 1) return;
+    flush(gcur, gstart, b1, first_seg);
 
-    // Last workgroup of this row group: every other slice has published.
-    __threadfence();
-    for (uint32_t i = threadIdx.x; i < M * kBlock; i += blockDim.x) {
-        const uint32_t t = i >> 7, rl = i & 127;
-        const float *src = ws + ((size_t)g * S * kGemvMaxM + t) * kBlock + rl;
-        float sum = __builtin_nontemporal_load(src);
-        for (uint32_t s2 = 1; s2 < S; s2++)
-            sum += __builtin_nontemporal_load(src + (size_t)s2 * kGemvMaxM * kBlock);
-        const uint32_t r2 = g * kBlock + rl;
-        if (r2 < sg.rows) sg.y[(size_t)t * sg.ldy + r2] = sum;
-    }
-    if (threadIdx.x == 0) p.cnt[sg.cnt_off + g] = 0u;
+    // ---- ordered sums of split groups this workgroup finished last ----
+    // Device-scope loads read the coherence point; each thread owns up to
+    // four outputs and fetches their partials four contributions at a time,
+    // adding them in range order.
+    auto reduce = [&](uint32_t G) {
+        const uint32_t cfirst = range_of((uint64_t)G * KB, T, P);
+        const uint32_t nc = range_of((uint64_t)G * KB + KB - 1, T, P) - cfirst + 1;
+        const uint32_t per_c = M * kBlock;
+        const float *base = p.ws + sg.ws_off + (size_t)G * sg.maxc * (kGemvMaxM * kBlock);
+        constexpr uint32_t kOut = kGemvMaxM * kBlock / kGemvThreads;   // 4
+        float sum[kOut];
+#pragma unroll
+        for (uint32_t o = 0; o < kOut; o++) sum[o] = 0.0f;
+        for (uint32_t c0 = 0; c0 < nc; c0 += 4) {
+            float v[4][kOut];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++)
+#pragma unroll
+                for (uint32_t o = 0; o < kOut; o++) {
+                    const uint32_t i = threadIdx.x + o * kGemvThreads;
+                    const uint32_t j = min(c0 + u, nc - 1);
+                    v[u][o] = i < per_c ? __hip_atomic_load(base + (size_t)j * kGemvMaxM * kBlock + i,
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                        : 0.0f;
+                }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++)
+#pragma unroll
+                for (uint32_t o = 0; o < kOut; o++)
+                    if (c0 + u < nc) sum[o] = (c0 + u == 0) ? v[u][o] : sum[o] + v[u][o];
+        }
+#pragma unroll
+        for (uint32_t o = 0; o < kOut; o++) {
+            const uint32_t i = threadIdx.x + o * kGemvThreads;
+            const uint32_t t = i >> 7, r2 = G * kBlock + (i & 127);
+            if (i < per_c && r2 < sg.rows) sg.y[(size_t)t * sg.ldy + r2] = sum[o];
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store(p.cnt + sg.cnt_off + G, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (pend0) reduce(pg0);
+    if (pend1) reduce(pg1);
 }
 
-uint32_t gemv_slices(uint32_t nb, uint32_t kb) {
-    // Aim for about two workgroups per CU on a 256-CU part, keep every slice
-    // at most kGemvMaxSliceKb blocks (LDS stage) and at least two blocks.
-    const uint32_t target = 512;
-    uint32_t s = (target + nb - 1) / nb;
-    const uint32_t s_min = (kb + kGemvMaxSliceKb - 1) / kGemvMaxSliceKb;
-    const uint32_t s_max = kb >= 2 ? kb / 2 : 1;
-    if (s > s_max) s = s_max;
-    if (s < s_min) s = s_min;
-    if (s < 1) s = 1;
-    if (s > kb) s = kb;
-    return s;
+uint32_t gemv_ctas(uint32_t nblocks, uint32_t cus, uint32_t per_cu) {
+    // A whole number of workgroups per CU keeps every CU's byte count equal;
+    // ranges are capped at kGemvMaxRangeBlocks (LDS stage at m = 8).
+    uint32_t P = cus * per_cu;
+    const uint32_t need = (nblocks + kGemvMaxRangeBlocks - 1) / kGemvMaxRangeBlocks;
+    if (P < need) P = ((need + cus - 1) / cus) * cus;
+    if (P > nblocks) P = nblocks;
+    return P;
 }
 
-hipError_t launch_gemv(const GemvParams &p, uint32_t grid, uint32_t max_slice_kb,
-                       hipStream_t stream) {
-    const size_t lds = (size_t)max_slice_kb * kBlock * 3 * p.m * 2;
-    hipLaunchKernelGGL(gemv_fp8_kernel, dim3(grid), dim3(kGemvThreads), lds, stream, p);
+uint32_t gemv_max_contrib(uint32_t nblocks, uint32_t nctas, uint32_t kb) {
+    // Ranges have at least floor(T/P) blocks, so a group of kb blocks meets
+    // at most ceil((kb - 1) / floor(T/P)) + 1 of them.
+    const uint32_t minlen = nblocks / nctas;
+    return (kb - 1 + minlen - 1) / minlen + 1;
+}
+
+size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks) {
+    return (size_t)range_blocks * kBlock * 3 * m * 2 + 16;   // + zero slot
+}
+
+hipError_t launch_gemv(const GemvParams &p, hipStream_t stream) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_fp8_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const size_t lds = gemv_lds_bytes(p.m, p.max_range);
+    if (lds > kGemvMaxLds) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemv_fp8_kernel, dim3(p.nctas), dim3(kGemvThreads), lds, stream, p);
     return hipGetLastError();
 }
 

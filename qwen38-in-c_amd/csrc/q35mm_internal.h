@@ -24,42 +24,58 @@ struct Weight {
 };
 
 // ---- decode GEMV (m <= 8 tokens) -------------------------------------
+// Stream-K decomposition: the weight's NB*KB 16 KiB blocks, taken in
+// (row group, K block) order and concatenated over up to four segments that
+// share K, are split into P equal contiguous ranges, one per workgroup.
 constexpr uint32_t kGemvMaxM = 8;
-constexpr uint32_t kGemvMaxSliceKb = 8;   // bounds the LDS activation stage
+constexpr uint32_t kGemvMaxRangeBlocks = 24;  // bounds the LDS stage (147 KiB at m = 8)
+constexpr uint32_t kGemvCtasPerCu = 2;        // default P = 2 workgroups per CU
+// Dynamic LDS cap: gfx950 gives a workgroup 160 KiB in total; 1 KiB stays
+// for the kernel's static LDS.
+constexpr uint32_t kGemvMaxLds = 159 * 1024;
 constexpr uint32_t kGemvThreads = 256;    // 4 wavefronts = one 128-row group
+constexpr uint32_t kGemvDepth = 4;        // K blocks of weights per wavefront ring
+constexpr uint32_t kGemvMaxPending = 4;   // groups one workgroup may have to reduce
 
+// Each segment (one weight) gets the grid it would get alone, so multi-weight
+// launches return exactly the bits of single-weight calls.
 struct GemvSeg {
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
     uint32_t rows;
     uint32_t ldy;
-    uint32_t ngroups;    // = NB
-    uint32_t nslices;    // split-K factor (depends on NB, KB only)
-    uint32_t cta_begin;  // first workgroup of this segment
-    uint32_t ws_off;     // float offset of this segment's partials
-    uint32_t cnt_off;    // offset of this segment's arrival counters
-    uint32_t pad_;
+    uint32_t nb;         // 128-row groups
+    uint32_t cta_begin;  // first workgroup of this segment's grid
+    uint32_t nctas;      // P: workgroups of this segment
+    uint32_t maxc;       // contributions per group the workspace holds
+    uint32_t ws_off;     // float offset of the segment's partials [nb][maxc][8][128]
+    uint32_t cnt_off;    // offset of the segment's arrival counters [nb]
 };
 
 struct GemvParams {
     GemvSeg seg[4];
     const float *x;      // [m][ldx] fp32
-    float *ws;           // split-K partials
+    float *ws;           // partial outputs
     uint32_t *cnt;       // arrival counters, zero between launches
     uint32_t ldx;
     uint32_t m;
     uint32_t k;          // valid columns
     uint32_t kb;         // KB
     uint32_t nseg;
+    uint32_t nctas;      // total workgroups
+    uint32_t max_range;  // longest range of any segment, in blocks
     uint32_t pad_;
 };
 
-// Split-K factor for an NB x KB weight; independent of m so that a batch
-// call returns exactly the bits of m single calls.
-uint32_t gemv_slices(uint32_t nb, uint32_t kb);
-hipError_t launch_gemv(const GemvParams &p, uint32_t grid, uint32_t max_slice_kb,
-                       hipStream_t stream);
+// P for T blocks on a device with cus compute units; depends only on the
+// weight shape, so a batch of m tokens gives exactly the bits of m single
+// calls.
+uint32_t gemv_ctas(uint32_t nblocks, uint32_t cus, uint32_t per_cu);
+// Most workgroups (P ranges) that can cover one group of kb blocks.
+uint32_t gemv_max_contrib(uint32_t nblocks, uint32_t nctas, uint32_t kb);
+size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks);
+hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 128;       // BM = BN = 128

@@ -79,6 +79,8 @@ struct Device {
     void *pin = nullptr;   // pinned host staging
     size_t pin_cap = 0;
     uint32_t gemm_min_m = 64;
+    uint32_t cus = 256;
+    uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
 };
 
@@ -102,10 +104,13 @@ int ensure_device() {
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
+    g_dev.cus = (uint32_t)prop.multiProcessorCount;
+    g_dev.gemv_per_cu = std::max(1u, env_u32("Q35MM_GEMV_CTAS_PER_CU", kGemvCtasPerCu));
     return Q35MM_OK;
 }
 
-hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g_dev.stream; }
+// Device-API streams follow the HIP convention: NULL is the null stream.
+hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
 // Grows a device buffer; waits for the device first because kernels queued
 // on any stream may still use the old allocation.
@@ -217,35 +222,37 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     p.k = cols;
     p.kb = KB;
     p.nseg = nseg;
-    uint32_t cta = 0, wsoff = 0, cntoff = 0, max_slice = 1;
+    uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &ws = w[s]->w;
-        const uint32_t S = gemv_slices(ws.nb, KB);
+        const uint32_t T = ws.nb * KB;
+        const uint32_t P = gemv_ctas(T, g_dev.cus, g_dev.gemv_per_cu);
         GemvSeg &g = p.seg[s];
         g.codes = ws.codes;
         g.scale = ws.scale;
         g.y = dY[s];
         g.rows = ws.rows;
         g.ldy = ws.rows;
-        g.ngroups = ws.nb;
-        g.nslices = S;
+        g.nb = ws.nb;
         g.cta_begin = cta;
+        g.nctas = P;
+        g.maxc = gemv_max_contrib(T, P, KB);
         g.ws_off = wsoff;
         g.cnt_off = cntoff;
-        cta += ws.nb * S;
-        if (S > 1) {
-            wsoff += ws.nb * S * kGemvMaxM * kBlock;
-            cntoff += ws.nb;
-        }
-        max_slice = std::max(max_slice, (KB + S - 1) / S);
+        cta += P;
+        wsoff += ws.nb * g.maxc * kGemvMaxM * kBlock;
+        cntoff += ws.nb;
+        max_range = std::max(max_range, (T + P - 1) / P);
     }
-    int rc = grow(g_dev.ws, (size_t)std::max(wsoff, 1u) * sizeof(float), false);
+    p.nctas = cta;
+    p.max_range = max_range;
+    int rc = grow(g_dev.ws, (size_t)wsoff * sizeof(float), false);
     if (rc) return rc;
-    rc = grow(g_dev.cnt, (size_t)std::max(cntoff, 1u) * sizeof(uint32_t), true);
+    rc = grow(g_dev.cnt, (size_t)cntoff * sizeof(uint32_t), true);
     if (rc) return rc;
     p.ws = (float *)g_dev.ws.ptr;
     p.cnt = (uint32_t *)g_dev.cnt.ptr;
-    HIP_TRY(launch_gemv(p, cta, max_slice, st));
+    HIP_TRY(launch_gemv(p, st));
     return Q35MM_OK;
 }
 
