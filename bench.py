@@ -106,6 +106,20 @@ def time_graph(torch, fn, steps: int, warmup: int, use_graph: bool):
     return t0.elapsed_time(t1) / 1e3, None
 
 
+def measured_traffic(profile: str):
+    """HBM bytes per launch of the decode GEMV from the committed rocprofv3
+    counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against a copy of
+    known size), or None if that summary is absent."""
+    path = os.path.join(ROOT, "profiles", profile)
+    try:
+        for ln in open(path):
+            if ln.startswith("traffic_bytes_per_launch"):
+                return int(ln.split()[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(wl, base, budget_s: float = 12.0):
     """The reference's compiled q35_mm.c (AVX2 + OpenMP), or the oracle port
     if the reference build is absent, on one layer at M=1."""
@@ -159,11 +173,14 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="first run one plain device-to-device copy of MIB MiB (a known-size reference "
+                         "kernel for hardware byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the FP8 matmul is sharded by rows across GPUs only in design; see DESIGN.md)",
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(a multi-GPU FP8 matmul would shard weights by 128-row groups; not built here)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -176,6 +193,16 @@ def main():
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    if args.calib_copy:
+        n = args.calib_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calib_copy} MiB read + {args.calib_copy} MiB written")
+        del src, dst
 
     steps = max(args.pool, (args.steps + args.pool - 1) // args.pool * args.pool)
     t = time.time()
@@ -211,7 +238,8 @@ def main():
     log(f"M=1: {value:.1f} GB/s, {ms_per_step * 1e3:.1f} us/step ({'graph' if g is not None else 'eager'})")
     n_launch = steps * len(base)
     roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("gemv_fp8_kernel_decode_m1_layer.md"),
             "kernel": "gemv_fp8_kernel", "launches": n_launch,
             "avg_launch_us": round(el / n_launch * 1e6, 3),
             "bytes_per_launch": step_bytes[1] // len(base)}

@@ -16,7 +16,7 @@
 //
 // Decomposition (stream-K).  A weight is a sequence of T = NB*KB 16 KiB
 // blocks (128-row group g, K block kb) in (g, kb) order.  Its grid is a
-// fixed P workgroups (two per CU by default); workgroup c takes the
+// fixed P workgroups (one per CU by default); workgroup c takes the
 // contiguous block range [c*T/P, (c+1)*T/P), so every CU streams the same
 // number of bytes whatever the shape.  Several weights sharing K (the
 // reference's multi4) get one grid each, concatenated into one launch.

@@ -29,7 +29,7 @@ struct Weight {
 // share K, are split into P equal contiguous ranges, one per workgroup.
 constexpr uint32_t kGemvMaxM = 8;
 constexpr uint32_t kGemvMaxRangeBlocks = 24;  // bounds the LDS stage (147 KiB at m = 8)
-constexpr uint32_t kGemvCtasPerCu = 2;        // default P = 2 workgroups per CU
+constexpr uint32_t kGemvCtasPerCu = 1;        // default P = one workgroup per CU
 // Dynamic LDS cap: gfx950 gives a workgroup 160 KiB in total; 1 KiB stays
 // for the kernel's static LDS.
 constexpr uint32_t kGemvMaxLds = 159 * 1024;
