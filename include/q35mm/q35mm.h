@@ -69,7 +69,9 @@ int q35mm_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
 int q35mm_gemv(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
                void *stream);
 /* Prefill GEMM for any m: activations rounded to bf16, bf16 MFMA with fp32
- * accumulation, fp32 block scale applied per 128-wide K step. */
+ * accumulation, fp32 block scale applied per 128-wide K step.  The bf16
+ * activations (m rounded up to 256 rows) and the resident weight must each
+ * stay under 4 GiB (Q35MM_EINVAL otherwise; q35mm_matmul then uses the GEMV). */
 int q35mm_gemm(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
                void *stream);
 /* Up to four weights sharing cols and X, one launch (rows may differ);

@@ -8,17 +8,23 @@
 //  - Activations are rounded to bf16 once per call by act_to_bf16_kernel,
 //    which writes them in the same lane-order layout as the weights (32-row
 //    tiles, 1 KiB per MFMA operand load).
-//  - e4m3 -> bf16 is exact, so weights are converted in registers after the
-//    LDS read; the block scale is never folded into bf16 weights (that
-//    would round).  Per 128-wide K block the MFMA accumulators hold the raw
-//    block product, then each output gets acc += scale * block (fp32 fmaf).
-//  - A workgroup computes a 128x128 output tile (one scale row-block, so the
-//    scale is uniform across the tile for each K block) with four
-//    wavefronts of 64x64; tiles of A (32 KiB bf16) and B (16 KiB e4m3) per K
-//    block are staged through LDS, the next block's global loads are in
-//    flight while the current one is multiplied.
-//  - Split-K with a deterministic last-arriver fixup when there are too few
-//    output tiles to occupy the device.
+//  - A workgroup computes a 256x256 output tile with eight wavefronts of
+//    128 (tokens) x 64 (weight rows), two per SIMD: 8 accumulators of 32x32,
+//    128 VGPRs, so the per-block rescale below is a plain v_mul.
+//  - K advances in stages of 64 columns (two 32-column chunks).  A stage is
+//    48 KiB of LDS: A as bf16 (32 KiB) and B still as e4m3 (16 KiB); B is
+//    widened to bf16 after the LDS read, exactly.  Stages are copied straight
+//    from global memory into a three-deep LDS ring with global_load_lds
+//    (no register staging), issued two stages ahead.
+//  - Block scales: a wavefront's 64 output columns lie in one 128-row scale
+//    block, so for each 128-wide K block its scale s is one number.  The
+//    accumulator is kept in units of the last nonzero scale: before block kb
+//    it is multiplied by s_prev / s_kb, after the last block by s_last.  One
+//    v_mul per accumulator and K block, and the scale is never folded into
+//    bf16 weights (that would round).  A block with scale 0 contributes
+//    nothing and is skipped.
+//  - Split-K with a deterministic last-arriver fixup when output tiles alone
+//    cannot occupy the device.
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
 
@@ -26,146 +32,293 @@ namespace q35mm {
 
 namespace {
 
-constexpr uint32_t kGemmThreads = 256;
-constexpr uint32_t kAPieces = 32;   // 4 m32 tiles x 4 chunks x 2 MFMA halves
-constexpr uint32_t kBPieces = 16;   // 4 n32 tiles x 4 chunks
-constexpr uint32_t kPiecesPerWave = (kAPieces + kBPieces) / 4;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-__device__ __forceinline__ u32x4_t ld16(const void *p) {
-    return *reinterpret_cast<const u32x4_t *>(p);
+constexpr uint32_t kStageK = 64;                          // two 32-column chunks
+constexpr uint32_t kStageA = kGemmTile * kStageK * 2;     // 32 KiB bf16
+constexpr uint32_t kStageB = kGemmTile * kStageK;         // 16 KiB e4m3
+constexpr uint32_t kStageBytes = kStageA + kStageB;       // 48 KiB
+constexpr uint32_t kRing = 3;
+constexpr uint32_t kTicketOff = kRing * kStageBytes;      // 144 KiB
+constexpr uint32_t kScaleOff = kTicketOff + 64;           // [2][kGemmMaxSliceKb] fp32
+constexpr uint32_t kGemmLds = kScaleOff + 2 * kGemmMaxSliceKb * 4;
+constexpr uint32_t kALoads = 4;    // 1 KiB pieces of A per wavefront per stage
+constexpr uint32_t kBLoads = 2;    // 1 KiB pieces of B per wavefront per stage
+constexpr uint32_t kStageLoads = kALoads + kBLoads;
+static_assert(8 * kALoads * kChunkBytes == kStageA, "A pieces");
+static_assert(8 * kBLoads * kChunkBytes == kStageB, "B pieces");
+static_assert(kGemmLds <= 160 * 1024, "LDS");
+
+// One wavefront copies 1 KiB: lane l's 16 bytes at g go to LDS l*16 past l.
+// The LDS address must be the same for all lanes (it goes through M0).
+// s_waitcnt immediate that waits only for vmcnt <= n (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr uint32_t waitcnt_vm(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
+constexpr uint32_t kWaitLgkm0 = 15u | (3u << 14) | (7u << 4);   // lgkmcnt(0) only
+
+// Plain s_barrier.  __syncthreads() adds workgroup fences that wait for every
+// outstanding global load (vmcnt(0)), which would drain the copies in flight
+// for the next stages; the caller waits for exactly the copies it needs.  The
+// barrier is a memory side effect to the compiler, so no LDS access moves
+// across it.
+__device__ __forceinline__ void lds_barrier() { __builtin_amdgcn_s_barrier(); }
+
+__device__ __forceinline__ void dma_1k(const uint8_t *g, lds_u8 *l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
 }
 
 }  // namespace
 
-// X fp32 [m][ldx] -> bf16 (round to nearest even) in lane order:
-//   unit u = ((m32 * KB + kb) * 8 + j*2 + q) * 64 + lane, 16 bytes each,
+// X fp32 [m][ldx] -> bf16 (round to nearest even) in lane order.  Output
+// unit u = ((m32 * KB + kb) * 8 + j*2 + q) * 64 + lane holds 16 bytes:
 //   row = m32*32 + lane%32, columns kb*128 + j*32 + (lane/32)*16 + q*8 + e.
+// One workgroup converts one 32-row x 128-column block: coalesced row reads
+// (512 B per row), a transpose through LDS, and 8 KiB of contiguous writes.
 // Rows >= m and columns >= k are zero.
 __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restrict__ x, uint32_t ldx,
                                                           uint32_t m, uint32_t k, uint32_t kb_total,
-                                                          uint32_t units, uint16_t *__restrict__ xb) {
-    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
-    if (u >= units) return;
-    const uint32_t lane = u & 63;
-    const uint32_t jq = (u >> 6) & 7;
-    const uint32_t rest = u >> 9;            // m32 * KB + kb
-    const uint32_t kb = rest % kb_total;
-    const uint32_t m32 = rest / kb_total;
-    const uint32_t row = m32 * 32 + (lane & 31);
-    const uint32_t col = kb * kBlock + (jq >> 1) * 32 + (lane >> 5) * 16 + (jq & 1) * 8;
-    uint32_t b[8];
-    const float *xp = x + (size_t)row * ldx + col;
+                                                          uint16_t *__restrict__ xb) {
+    __shared__ __align__(16) uint16_t t[32][128 + 8];     // +8: spread rows over banks
+    const uint32_t kb = blockIdx.x % kb_total;
+    const uint32_t m32 = blockIdx.x / kb_total;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float v = (row < m && col + e < k) ? xp[e] : 0.0f;
-        b[e] = f32_to_bf16_rne(v);
+    for (uint32_t i = 0; i < 4; i++) {
+        const uint32_t idx = threadIdx.x + 256 * i;        // 32 rows x 32 float4
+        const uint32_t r = idx >> 5, c4 = idx & 31;
+        const uint32_t row = m32 * 32 + r, col = kb * kBlock + c4 * 4;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (row < m) {
+            const float *xp = x + (size_t)row * ldx + col;
+            if (col + 4 <= k && ((reinterpret_cast<uintptr_t>(xp) & 15) == 0)) {
+                const float4 f = *reinterpret_cast<const float4 *>(xp);
+                v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            } else {
+#pragma unroll
+                for (uint32_t e = 0; e < 4; e++)
+                    if (col + e < k) v[e] = xp[e];
+            }
+        }
+        u32x2_t w = {f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16),
+                     f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16)};
+        *reinterpret_cast<u32x2_t *>(&t[r][c4 * 4]) = w;
     }
-    u32x4_t o = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-    *reinterpret_cast<u32x4_t *>(xb + (size_t)u * 8) = o;
+    __syncthreads();
+    uint8_t *out = reinterpret_cast<uint8_t *>(xb) + ((size_t)m32 * kb_total + kb) * 8 * kChunkBytes;
+#pragma unroll
+    for (uint32_t i = 0; i < 2; i++) {
+        const uint32_t u = threadIdx.x + 256 * i;           // 0..511
+        const uint32_t lane = u & 63, jq = u >> 6;
+        const uint32_t r = lane & 31, c = (jq >> 1) * 32 + (lane >> 5) * 16 + (jq & 1) * 8;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t *>(&t[r][c]);
+        *reinterpret_cast<u32x4_t *>(out + u * 16) = v;
+    }
 }
 
 __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
-    __shared__ __align__(16) uint8_t lds_a[kAPieces * kChunkBytes];
-    __shared__ __align__(16) uint8_t lds_b[kBPieces * kChunkBytes];
-    __shared__ uint32_t s_ticket;
+    extern __shared__ __align__(16) uint8_t lds[];
+    lds_u8 *const ring = (lds_u8 *)lds;
 
     const uint32_t S = p.nslices;
     const uint32_t tile = blockIdx.x / S;
-    const uint32_t s = blockIdx.x - tile * S;
+    const uint32_t sl = blockIdx.x - tile * S;
     const uint32_t mt = tile % p.mtiles;
     const uint32_t nt = tile / p.mtiles;
     const uint32_t KB = p.kb;
-    const uint32_t kb0 = (s * KB) / S;
-    const uint32_t kb1 = ((s + 1) * KB) / S;
+    const uint32_t kb0 = (sl * KB) / S, kb1 = ((sl + 1) * KB) / S;
+    const uint32_t st0 = 2 * kb0, st1 = 2 * kb1;   // stages of 64 columns
 
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wv = threadIdx.x >> 6;
-    const uint32_t wm = wv & 1, wn = wv >> 1;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wm = wv & 1, wn = wv >> 1;   // 2 x 4 wavefronts of 128 x 64
 
-    // Global sources for the pieces this wavefront copies.  Piece P < 32 is
-    // A piece (m32 = P/8, chunk-half = P%8); P >= 32 is B piece P-32.
+    // ---- global sources of this wavefront's pieces ----
+    // A piece P (0..31): token rows (mt*8 + P/4)*32.., piece (h*4 + P%4) of the
+    // K block's eight (h = stage half); wavefront w copies 4w..4w+3.
+    // B piece Q (0..15): weight rows (nt*8 + Q/2)*32.., chunk 2h + Q%2;
+    // wavefront w copies 2w, 2w+1.  A missing second row group (odd NB)
+    // reads the last group instead; those columns are never stored.
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb);
-    const size_t a_tile_stride = (size_t)KB * 8 * kChunkBytes;   // one m32 row of tiles
-    u32x4_t stage[kPiecesPerWave];
-    auto load_stage = [&](uint32_t kb) {
+    // Byte offsets (32-bit: the host keeps both operands under 4 GiB) that are
+    // wavefront-uniform, so they live in scalar registers; each copy adds the
+    // lane's 16 bytes and uses the global_load_lds saddr + voffset form.
+    uint32_t aoff[kALoads], boff[kBLoads];
+    const uint32_t lane16 = lane * 16;
 #pragma unroll
-        for (uint32_t u = 0; u < kPiecesPerWave; u++) {
-            const uint32_t P = wv + 4 * u;
-            const uint8_t *src;
-            if (P < kAPieces) {
-                const uint32_t m32 = mt * 4 + P / 8;
-                src = xa + m32 * a_tile_stride + (size_t)kb * 8 * kChunkBytes + (P % 8) * kChunkBytes;
-            } else {
-                src = p.codes + ((size_t)nt * KB + kb) * kBlockBytes + (P - kAPieces) * kChunkBytes;
-            }
-            stage[u] = ld16(src + lane * 16);
-        }
-    };
-    auto store_stage = [&]() {
-#pragma unroll
-        for (uint32_t u = 0; u < kPiecesPerWave; u++) {
-            const uint32_t P = wv + 4 * u;
-            uint8_t *dst = P < kAPieces ? lds_a + P * kChunkBytes : lds_b + (P - kAPieces) * kChunkBytes;
-            *reinterpret_cast<u32x4_t *>(dst + lane * 16) = stage[u];
-        }
-    };
-
-    f32x16_t acc[2][2] = {};
-    const f32x16_t zero = {};
-    const float *srow = p.scale + (size_t)nt * KB;
-
-    load_stage(kb0);
-    for (uint32_t kb = kb0; kb < kb1; kb++) {
-        __syncthreads();
-        store_stage();
-        __syncthreads();
-        if (kb + 1 < kb1) load_stage(kb + 1);
-
-        f32x16_t part[2][2];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            u32x4_t braw[2];
-#pragma unroll
-            for (int jn = 0; jn < 2; jn++)
-                braw[jn] = ld16(lds_b + ((2 * wn + jn) * 4 + j) * kChunkBytes + lane * 16);
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-                bf16x8_t bop[2];
-#pragma unroll
-                for (int jn = 0; jn < 2; jn++)
-                    bop[jn] = e4m3x8_to_bf16x8(braw[jn][2 * q], braw[jn][2 * q + 1]);
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const bf16x8_t aop = __builtin_bit_cast(
-                        bf16x8_t, ld16(lds_a + ((2 * wm + i) * 8 + j * 2 + q) * kChunkBytes + lane * 16));
-#pragma unroll
-                    for (int jn = 0; jn < 2; jn++)
-                        part[i][jn] = mfma32x32x16(aop, bop[jn], (j == 0 && q == 0) ? zero : part[i][jn]);
-                }
-            }
-        }
-        const float sc = srow[kb];
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int jn = 0; jn < 2; jn++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][jn][r] = __builtin_fmaf(sc, part[i][jn][r], acc[i][jn][r]);
+    for (uint32_t i = 0; i < kALoads; i++) {
+        const uint32_t P = wv * kALoads + i;
+        aoff[i] = (mt * 8 + P / 4) * (KB * 8 * kChunkBytes) + (P % 4) * kChunkBytes;
     }
+#pragma unroll
+    for (uint32_t i = 0; i < kBLoads; i++) {
+        const uint32_t Q = wv * kBLoads + i;
+        const uint32_t n32 = Q / 2;
+        const uint32_t nbk = min(nt * 2 + n32 / 4, p.nb - 1);
+        boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
+    }
+    auto issue = [&](uint32_t st, uint32_t buf) {
+        const uint32_t kb = st >> 1, h = st & 1;
+        lds_u8 *la = ring + buf * kStageBytes;
+#pragma unroll
+        for (uint32_t i = 0; i < kALoads; i++)
+            dma_1k(xa + (aoff[i] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
+                   la + (wv * kALoads + i) * kChunkBytes);
+#pragma unroll
+        for (uint32_t i = 0; i < kBLoads; i++)
+            dma_1k(p.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
+                   la + kStageA + (wv * kBLoads + i) * kChunkBytes);
+    };
+
+    // ---- block scales of the tile's two row groups, staged in LDS ----
+    // Read from LDS inside the loop they keep the LDS counter in order (a
+    // scalar load completing out of order would force full waits) and stay
+    // off the vmcnt queue that counts the stage copies.  0 past the last row
+    // group.  Done before the first copy is issued, so this barrier drains
+    // nothing.
+    float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
+    for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
+        const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
+        const uint32_t nbg = nt * 2 + g;
+        float v = 0.0f;
+        if (nbg < p.nb && kk < kb1 - kb0) v = p.scale[(size_t)nbg * KB + kb0 + kk];
+        sc_lds[j] = v;
+    }
+    __syncthreads();
+    const float *my_sc = sc_lds + (wn >> 1) * kGemmMaxSliceKb - kb0;   // indexed by kb
+
+    f32x16_t acc[4][2] = {};
+    float s_prev = 0.0f;
+
+    // Operands of one 32-column chunk: A for this wavefront's 4 token
+    // sub-tiles x 2 MFMA halves (bf16), B for its 2 weight sub-tiles (16 e4m3
+    // codes per lane, both halves).
+    struct Frags {
+        bf16x8_t a[4][2];
+        u32x4_t b[2];
+    };
+    auto read_frags = [&](Frags &f, uint32_t buf, uint32_t jj) {
+        const uint8_t *la = lds + buf * kStageBytes;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++)
+#pragma unroll
+            for (uint32_t q = 0; q < 2; q++)
+                f.a[i][q] = *reinterpret_cast<const bf16x8_t *>(
+                    la + (((wm * 4 + i) * 2 + jj) * 2 + q) * kChunkBytes + lane * 16);
+#pragma unroll
+        for (uint32_t jn = 0; jn < 2; jn++)
+            f.b[jn] = *reinterpret_cast<const u32x4_t *>(
+                la + kStageA + ((wn * 2 + jn) * 2 + jj) * kChunkBytes + lane * 16);
+    };
+    // 16 MFMAs; the two halves of a chunk are issued 8 apart so no MFMA waits
+    // for the one before it.  keep is the conversion's power-of-two scale:
+    // 1.0 (exact) for a live block, 0.0 (= 2^-127) for a block whose scale is
+    // 0, which then adds at most 2^-127 * 448 * |x| per term (and NaN for a
+    // NaN code, as lut[code] * 0 does).
+    auto mma = [&](const Frags &f, bool rescale, float r, float keep) {
+        bf16x8_t bw[2][2];
+#pragma unroll
+        for (uint32_t jn = 0; jn < 2; jn++) {
+            bw[jn][0] = e4m3x8_to_bf16x8_cvt(f.b[jn][0], f.b[jn][1], keep);
+            bw[jn][1] = e4m3x8_to_bf16x8_cvt(f.b[jn][2], f.b[jn][3], keep);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 2; q++)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+#pragma unroll
+                for (uint32_t jn = 0; jn < 2; jn++) {
+                    if (q == 0 && rescale) acc[i][jn] *= r;
+                    acc[i][jn] = mfma32x32x16(f.a[i][q], bw[jn][q], acc[i][jn]);
+                }
+    };
+
+    // ---- pipeline ----
+    // LDS ring of three stages.  Stage s: its first chunk's operands are in
+    // registers (f0) when it starts; the second chunk's are read (f1) while
+    // the first chunk's MFMAs run.  Then, once every wavefront has read all of
+    // stage s and stage s+1 has landed (one barrier), stage s+3 is copied
+    // into s's slot and stage s+1's first chunk is read while the second
+    // chunk's MFMAs run.  Every wavefront issues exactly kStageLoads copies
+    // per stage (clamped to the last stage past the end), so
+    // "vmcnt <= kStageLoads" means: all but the newest stage have landed.
+    issue(st0, 0);
+    issue(min(st0 + 1, st1 - 1), 1);
+    issue(min(st0 + 2, st1 - 1), 2);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
+    lds_barrier();
+    Frags f0, f1;
+    read_frags(f0, 0, 0);
+    uint32_t buf = 0;
+    // No branches around the MFMAs: a block with scale 0 runs with keep = 0
+    // and r = 1, so the accumulator keeps its units.
+    // sched_barrier(0) pins the phases: the compiler would otherwise sink each
+    // LDS read next to its MFMA and wait for it there.  The next K block's
+    // scale is read with the f1 operands and its rescale factor computed after
+    // the MFMAs were issued, so neither waits.
+    float sc0 = my_sc[kb0];
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    bool live = sc0 != 0.0f;
+    float keep = live ? 1.0f : 0.0f;
+    float r = live ? 0.0f : 1.0f;            // the accumulator is still zero
+    s_prev = live ? sc0 : 0.0f;              // units of the accumulator after this block
+    for (uint32_t kb = kb0; kb < kb1; kb++) {
+        bool live_n = false;
+        float keep_n = 0.0f;
+        float r_n = 1.0f, s_prev_n = s_prev;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t s = 2 * kb + h;
+            // f0 was read a whole MFMA phase ago.  Waiting for it here, before
+            // f1's reads are issued, keeps the MFMAs below free of waits (the
+            // compiler cannot count LDS reads past the LDS copies and would
+            // otherwise wait for f1 too).
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            read_frags(f1, buf, 1);
+            float sc_n = 0.0f;
+            if (h == 0) sc_n = my_sc[min(kb + 1, kb1 - 1)];
+            __builtin_amdgcn_sched_barrier(0);
+            mma(f0, h == 0, r, keep);
+            __builtin_amdgcn_sched_barrier(0);
+            if (h == 0) {
+                live_n = kb + 1 < kb1 && sc_n != 0.0f;
+                keep_n = live_n ? 1.0f : 0.0f;
+                r_n = live_n ? (s_prev != 0.0f ? s_prev / sc_n : 0.0f) : 1.0f;
+                s_prev_n = live_n ? sc_n : s_prev;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f1 is in registers: slot s is free
+            lds_barrier();
+            issue(min(s + 3, st1 - 1), buf);
+            buf = buf == 2 ? 0 : buf + 1;
+            read_frags(f0, buf, 0);                    // past the end: unused, in bounds
+            __builtin_amdgcn_sched_barrier(0);
+            mma(f1, false, 1.0f, keep);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        live = live_n;
+        keep = keep_n;
+        r = r_n;
+        s_prev = s_prev_n;
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));   // no copy outlives the loop
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++)
+#pragma unroll
+        for (uint32_t jn = 0; jn < 2; jn++) acc[i][jn] *= s_prev;
 
     // Output coordinates of accumulator element (i, jn, r) of this lane.
-    auto out_row = [&](int i, int r) -> uint32_t {
-        return (2 * wm + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    auto out_row = [&](uint32_t i, uint32_t r) -> uint32_t {
+        return wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     };
-    auto out_col = [&](int jn) -> uint32_t { return (2 * wn + jn) * 32 + (lane & 31); };
+    auto out_col = [&](uint32_t jn) -> uint32_t { return wn * 64 + jn * 32 + (lane & 31); };
 
     if (S == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (uint32_t i = 0; i < 4; i++)
 #pragma unroll
-            for (int jn = 0; jn < 2; jn++)
+            for (uint32_t jn = 0; jn < 2; jn++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
+                for (uint32_t r = 0; r < 16; r++) {
                     const uint32_t mrow = mt * kGemmTile + out_row(i, r);
                     const uint32_t ncol = nt * kGemmTile + out_col(jn);
                     if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = acc[i][jn][r];
@@ -173,51 +326,76 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         return;
     }
 
-    float *ws = p.ws + ((size_t)tile * S + s) * kGemmTile * kGemmTile;
+    // ---- split-K: publish, ticket, ordered sum by the last slice ----
+    // Device-scope atomic stores reach the coherence point (no L2 writeback
+    // needed to publish); the last workgroup to arrive adds the slices in
+    // order, so the result does not depend on timing.
+    constexpr uint32_t kTileElems = kGemmTile * kGemmTile;
+    float *part = p.ws + ((size_t)tile * S + sl) * kTileElems;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (uint32_t i = 0; i < 4; i++)
 #pragma unroll
-        for (int jn = 0; jn < 2; jn++)
+        for (uint32_t jn = 0; jn < 2; jn++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) ws[out_row(i, r) * kGemmTile + out_col(jn)] = acc[i][jn][r];
-    __threadfence();
+            for (uint32_t r = 0; r < 16; r++)
+                __hip_atomic_store(part + out_row(i, r) * kGemmTile + out_col(jn), acc[i][jn][r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) s_ticket = atomicAdd(p.cnt + tile, 1u);
+    uint32_t *ticket = reinterpret_cast<uint32_t *>(lds + kTicketOff);
+    if (threadIdx.x == 0)
+        *ticket = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s_ticket != S - 1) return;
+    if (*ticket != S - 1) return;
 
-    __threadfence();
-    const float *base = p.ws + (size_t)tile * S * kGemmTile * kGemmTile;
-    for (uint32_t e = threadIdx.x; e < kGemmTile * kGemmTile; e += blockDim.x) {
-        float sum = __builtin_nontemporal_load(base + e);
+    const float *base = p.ws + (size_t)tile * S * kTileElems;
+    for (uint32_t e = threadIdx.x * 4; e < kTileElems; e += kGemmThreads * 4) {
+        float sum[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; u++)
+            sum[u] = __hip_atomic_load(base + e + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (uint32_t s2 = 1; s2 < S; s2++)
-            sum += __builtin_nontemporal_load(base + (size_t)s2 * kGemmTile * kGemmTile + e);
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++)
+                sum[u] += __hip_atomic_load(base + (size_t)s2 * kTileElems + e + u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t mrow = mt * kGemmTile + e / kGemmTile;
-        const uint32_t ncol = nt * kGemmTile + e % kGemmTile;
-        if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = sum;
+#pragma unroll
+        for (uint32_t u = 0; u < 4; u++) {
+            const uint32_t ncol = nt * kGemmTile + (e + u) % kGemmTile;
+            if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = sum[u];
+        }
     }
-    if (threadIdx.x == 0) p.cnt[tile] = 0u;
+    if (threadIdx.x == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 uint32_t gemm_slices(uint32_t mtiles, uint32_t ntiles, uint32_t kb) {
-    // Split K only when the output tiles cannot occupy a 256-CU device.
+    // Split K only when the output tiles cannot occupy a 256-CU device; each
+    // slice keeps at least four K blocks and at most kGemmMaxSliceKb (the
+    // slice's scales are staged in LDS).
     const uint32_t tiles = mtiles * ntiles;
     uint32_t s = 1;
-    while (tiles * s < 256 && s * 2 <= kb / 4) s *= 2;
+    while (tiles * (s + 1) <= 256 && (s + 1) * 4 <= kb) s++;
+    while ((kb + s - 1) / s > kGemmMaxSliceKb) s++;
     return s;
 }
 
-hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
-                              uint32_t mtiles, uint32_t kb, uint16_t *xb, hipStream_t stream) {
-    const uint32_t units = mtiles * 4 * kb * 8 * 64;
-    hipLaunchKernelGGL(act_to_bf16_kernel, dim3((units + 255) / 256), dim3(256), 0, stream,
-                       x, ldx, m, k, kb, units, xb);
+hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k, uint32_t m32_tiles,
+                              uint32_t kb, uint16_t *xb, hipStream_t stream) {
+    hipLaunchKernelGGL(act_to_bf16_kernel, dim3(m32_tiles * kb), dim3(256), 0, stream, x, ldx, m, k, kb, xb);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
     const uint32_t grid = p.mtiles * p.ntiles * p.nslices;
-    hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), 0, stream, p);
+    hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
     return hipGetLastError();
 }
 

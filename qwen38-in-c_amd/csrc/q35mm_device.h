@@ -70,6 +70,23 @@ __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Eight e4m3 codes -> bf16x8 with gfx950's v_cvt_scalef32_pk_bf16_fp8 (two
+// codes per instruction; half the VALU of the path above).  The instruction
+// scales by 2^exponent(scale) only (E8M0 semantics: 1.5 acts as 1, 0 as
+// 2^-127).  With scale 1.0 every finite e4m3 value is exact in bf16, so the
+// result equals the one above (checked for all 256 codes); 0x7F / 0xFF give
+// NaN.
+__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8_cvt(uint32_t w0, uint32_t w1, float pow2_scale) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, pow2_scale, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, pow2_scale, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, pow2_scale, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, pow2_scale, true);
+    const u32x4_t v = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                       __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     uint32_t u = f32_bits(f);

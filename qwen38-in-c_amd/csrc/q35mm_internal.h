@@ -78,10 +78,12 @@ size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks);
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
-constexpr uint32_t kGemmTile = 128;       // BM = BN = 128
+constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
+constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64
+constexpr uint32_t kGemmMaxSliceKb = 1024;  // K blocks one workgroup may cover
 
 struct GemmParams {
-    const uint16_t *xb;  // lane-order bf16 activations, mtiles*128 rows
+    const uint16_t *xb;  // lane-order bf16 activations, mtiles*256 rows
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
@@ -91,16 +93,17 @@ struct GemmParams {
     uint32_t rows;
     uint32_t ldy;
     uint32_t kb;
+    uint32_t nb;         // 128-row groups of the weight
     uint32_t mtiles;
     uint32_t ntiles;
     uint32_t nslices;
-    uint32_t pad_;
 };
 
 uint32_t gemm_slices(uint32_t mtiles, uint32_t ntiles, uint32_t kb);
-// X [m][ldx] fp32 -> lane-order bf16 [mtiles*128 rows][kb*128 cols].
+// X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
+// multiple of 32 (m32 tiles = rows_pad / 32).
 hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
-                              uint32_t mtiles, uint32_t kb, uint16_t *xb,
+                              uint32_t m32_tiles, uint32_t kb, uint16_t *xb,
                               hipStream_t stream);
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
 

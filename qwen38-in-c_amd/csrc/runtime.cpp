@@ -269,9 +269,20 @@ int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const floa
     return Q35MM_OK;
 }
 
+// The GEMM kernel addresses both operands with 32-bit byte offsets.
+bool gemm_fits(const Weight &w, uint32_t m) {
+    const uint64_t mtiles = (m + kGemmTile - 1) / kGemmTile;
+    const uint64_t xb_bytes = mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
+    const uint64_t w_bytes = (uint64_t)w.nb * w.kb * kBlockBytes;
+    return xb_bytes <= UINT32_MAX && w_bytes <= UINT32_MAX;
+}
+
 int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hipStream_t st) {
     const Weight &w = wt->w;
+    if (!gemm_fits(w, m))
+        return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
     const uint32_t mtiles = (m + kGemmTile - 1) / kGemmTile;
+    const uint32_t ntiles = (w.nb + 1) / 2;   // 256 output columns = two 128-row groups
     const size_t xb_bytes = (size_t)mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
     int rc = grow(g_dev.xb, xb_bytes, false);
     if (rc) return rc;
@@ -284,10 +295,11 @@ int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hip
     p.rows = w.rows;
     p.ldy = w.rows;
     p.kb = w.kb;
+    p.nb = w.nb;
     p.mtiles = mtiles;
-    p.ntiles = w.nb;
-    p.nslices = gemm_slices(mtiles, w.nb, w.kb);
-    const size_t tiles = (size_t)mtiles * w.nb;
+    p.ntiles = ntiles;
+    p.nslices = gemm_slices(mtiles, ntiles, w.kb);
+    const size_t tiles = (size_t)mtiles * ntiles;
     if (p.nslices > 1) {
         rc = grow(g_dev.ws, tiles * p.nslices * kGemmTile * kGemmTile * sizeof(float), false);
         if (rc) return rc;
@@ -296,7 +308,7 @@ int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hip
     if (rc) return rc;
     p.ws = (float *)g_dev.ws.ptr;
     p.cnt = (uint32_t *)g_dev.cnt.ptr;
-    HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles, w.kb, (uint16_t *)g_dev.xb.ptr, st));
+    HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles * (kGemmTile / kSubRows), w.kb, (uint16_t *)g_dev.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -308,7 +320,7 @@ int check_weight(const q35mm_weight *w) {
 
 int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hipStream_t st) {
     if (m == 0) return Q35MM_OK;
-    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0) return run_gemm(w, m, dX, dY, st);
+    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(w->w, m)) return run_gemm(w, m, dX, dY, st);
     const q35mm_weight *ws[1] = {w};
     float *ys[1] = {dY};
     return run_gemv(ws, 1, m, dX, ys, st);
@@ -690,7 +702,9 @@ Q35MM_API int q35mm_matmul_multi(const q35mm_weight *const *w, uint32_t nseg, ui
     }
     if (m == 0) return Q35MM_OK;
     hipStream_t st = pick_stream(stream);
-    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0) {
+    bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0;
+    for (uint32_t s = 0; s < nseg && gemm; s++) gemm = gemm_fits(w[s]->w, m);
+    if (gemm) {
         for (uint32_t s = 0; s < nseg; s++) {
             rc = run_gemm(w[s], m, dX, dY[s], st);
             if (rc) return rc;
