@@ -73,12 +73,21 @@ __device__ __forceinline__ StageItem stage_item(uint32_t i, uint32_t per_t, uint
 
 // Raw loads of one item; the address is clamped into the row so the loads
 // are unconditional (no branch between them and the weight prologue).  The
-// caller zeroes columns >= k before use (stage_mask).
+// caller zeroes columns >= k before use (stage_mask).  With vec (x 16-byte
+// aligned, ldx % 4 == 0, k % 8 == 0) an item is two 16-byte loads at the
+// clamped column min(kg, k - 8); otherwise eight 4-byte loads.
 __device__ __forceinline__ void stage_load(float (&xv)[8], const float *x, uint32_t ldx, uint32_t k,
-                                           const StageItem &it) {
+                                           const StageItem &it, bool vec) {
     const float *xp = x + (size_t)it.t * ldx;
+    if (vec) {
+        const float4 *v = reinterpret_cast<const float4 *>(xp + min(it.kg, k - 8));
+        const float4 a = v[0], b = v[1];
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; e++) xv[e] = xp[min(it.kg + e, k - 1)];
+        for (int e = 0; e < 8; e++) xv[e] = xp[min(it.kg + e, k - 1)];
+    }
 }
 
 __device__ __forceinline__ void stage_mask(float (&xv)[8], uint32_t k, const StageItem &it) {
@@ -163,7 +172,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     float xpre[kStagePre][8];
 #pragma unroll
     for (uint32_t u = 0; u < kStagePre; u++)   // index clamped: loads are unconditional
-        stage_load(xpre[u], p.x, p.ldx, p.k, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0));
+        stage_load(xpre[u], p.x, p.ldx, p.k, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0),
+                   p.x_vec != 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], scs[d], min(b0 + d, b1 - 1));
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     for (uint32_t i = threadIdx.x + kStagePre * kGemvThreads; i < nvec; i += kGemvThreads) {
         const StageItem it = stage_item(i, per_t, KB, b0);
         float xv[8];
-        stage_load(xv, p.x, p.ldx, p.k, it);
+        stage_load(xv, p.x, p.ldx, p.k, it, p.x_vec != 0);
         stage_mask(xv, p.k, it);
         stage_store(lds, M, it, xv);
     }

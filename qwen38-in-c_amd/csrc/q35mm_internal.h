@@ -65,7 +65,7 @@ struct GemvParams {
     uint32_t nseg;
     uint32_t nctas;      // total workgroups
     uint32_t max_range;  // longest range of any segment, in blocks
-    uint32_t pad_;
+    uint32_t x_vec;      // x 16-byte aligned, ldx % 4 == 0, k % 8 == 0: vector staging loads
 };
 
 // P for T blocks on a device with cus compute units; depends only on the

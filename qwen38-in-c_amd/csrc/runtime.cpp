@@ -222,6 +222,7 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     p.k = cols;
     p.kb = KB;
     p.nseg = nseg;
+    p.x_vec = ((reinterpret_cast<uintptr_t>(dX) & 15) == 0 && cols % 8 == 0) ? 1u : 0u;
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &ws = w[s]->w;
