@@ -5,13 +5,19 @@
 
 One step = one pass of the decode hot path over one layer at M=1 token: the
 five projections 5120->6144 (qkv), 4096->5120 (o_proj), 5120->17408 (gate),
-5120->17408 (up), 17408->5120 (down), each one launch of the decode GEMV
-kernel, with weights and activations resident in HBM before timing starts.
-Steps rotate over a pool of P distinct layer copies (default 8 x 320 MB =
-2.56 GB) so the 256 MB Infinity Cache and the L2 cannot serve repeats.  The
-P copies are one generated layer with per-row sign patterns flipped
-(code ^ 0x80 on a pseudo-random half of the rows), so every copy is distinct
-data of the same distribution.
+5120->17408 (up), 17408->5120 (down), called as the reference's decode
+calls them: gate and up share x and go through one q35_mm_fp8_multi4-style
+call (qwen35-c/src/q35_model.c:930-934), the others one call each -- four
+launches of the decode GEMV kernel, with weights and activations resident in
+HBM before timing starts.  Steps rotate over a pool of P distinct layer
+copies (default 8 x 320 MB = 2.56 GB) so the 256 MB Infinity Cache and the
+L2 cannot serve repeats.  The copies are one generated layer with per-row
+sign patterns flipped (code ^ 0x80 on a pseudo-random half of the rows), so
+every copy is distinct data of the same distribution.
+
+Also the full decode-token weight stream: a stack of 64 such layers (20.5 GB
+of distinct FP8 weights resident) run back to back at M=1, 256 launches per
+token (--stack-layers, 0 to skip).
 
 value = algorithmic bytes of K steps / elapsed seconds (HIP events on the
 launch stream, launches replayed from a HIP graph), in GB/s.  Algorithmic
@@ -53,7 +59,8 @@ def row_sign_mask(n: int, variant: int):
 
 
 def make_layer_pool(q, wl, pool: int):
-    """pool x {qkv, o_proj, gate, up, down} resident weights + host base."""
+    """pool x {qkv, o_proj, gate, up, down} resident weights + host base.
+    Copy v is the base layer with row_sign_mask(n, v) applied."""
     base = []
     for i, (name, k, n) in enumerate(wl.DECODE_SHAPES):
         t = time.time()
@@ -134,15 +141,25 @@ def cpu_baseline(wl, base, budget_s: float = 12.0):
         impl, kind = Oracle(), "port"
         run = impl.mm
     xs = [wl.gen_act(7 + i, 1, k)[0] for i, (_, k, _, _, _) in enumerate(base)]
+    xs[3] = xs[2]                      # gate and up share x
     layer_bytes = sum(wl.algorithmic_bytes(1, k, n) for _, k, n, _, _ in base)
-    for (name, k, n, W, sc), x in zip(base, xs):   # warm: page in, spin up threads
-        run(W, sc, x)
+
+    def layer():
+        # as the reference's decode: gate and up in one multi4 call
+        for j in (0, 1):
+            run(base[j][3], base[j][4], xs[j])
+        if kind == "reference":
+            impl.multi4([base[2][3], base[3][3]], [base[2][4], base[3][4]], xs[2])
+        else:
+            run(base[2][3], base[2][4], xs[2])
+            run(base[3][3], base[3][4], xs[3])
+        run(base[4][3], base[4][4], xs[4])
+    layer()   # warm: page in, spin up threads
     times = []
     t_end = time.time() + budget_s
     while time.time() < t_end or len(times) < 3:
         t = time.perf_counter()
-        for (name, k, n, W, sc), x in zip(base, xs):
-            run(W, sc, x)
+        layer()
         times.append(time.perf_counter() - t)
         if len(times) >= 200:
             break
@@ -156,7 +173,7 @@ def cpu_baseline(wl, base, budget_s: float = 12.0):
     except OSError:
         pass
     return {"value": round(layer_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{len(times)} passes of one layer's 5 projections at M=1 "
+            "sample": f"{len(times)} passes of one layer's 5 projections at M=1 (gate+up via multi4) "
                       f"({layer_bytes / 1e6:.1f} MB), median {med * 1e3:.2f} ms/pass; "
                       f"{'oracle/_ref q35_mm.c' if kind == 'reference' else 'oracle port'}, "
                       f"OMP_NUM_THREADS={threads}, host CPU: {cpu}"}
@@ -173,6 +190,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--stack-layers", type=int, default=64,
+                    help="distinct layers of the full-token weight stream (0: skip)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="first run one plain device-to-device copy of MIB MiB (a known-size reference "
                          "kernel for hardware byte counters)")
@@ -206,25 +225,37 @@ def main():
 
     steps = max(args.pool, (args.steps + args.pool - 1) // args.pool * args.pool)
     t = time.time()
-    base, layers = make_layer_pool(q, wl, args.pool)
-    log(f"pool of {args.pool} layers resident ({sum(w.nbytes for w in layers[0]) * args.pool / 1e9:.2f} GB) "
-        f"in {time.time() - t:.1f}s")
+    n_lay = max(args.pool, args.stack_layers)
+    base, stack = make_layer_pool(q, wl, n_lay)
+    layers = stack[: args.pool]
+    log(f"{n_lay} distinct layers resident ({sum(w.nbytes for w in stack[0]) * n_lay / 1e9:.2f} GB) "
+        f"in {time.time() - t:.1f}s; the first {args.pool} are the headline pool")
 
-    def decode_step_fn(m: int):
+    # Projection order in DECODE_SHAPES: qkv, o_proj, gate, up, down; gate
+    # and up read the same x.
+    GATE, UP = 2, 3
+
+    def layer_call(L, xs, ys, m):
+        q.gemv(L[0], xs[0], ys[0], m=m)
+        q.gemv(L[1], xs[1], ys[1], m=m)
+        q.matmul_multi([L[GATE], L[UP]], xs[GATE], [ys[GATE], ys[UP]], m=m)
+        q.gemv(L[4], xs[4], ys[4], m=m)
+
+    def decode_step_fn(m: int, lays, nout: int):
         xs = [torch.from_numpy(wl.gen_act(100 + i, m, k)).to(dev) for i, (_, k, _, _, _) in enumerate(base)]
+        xs[UP] = xs[GATE]
         ys = [[torch.empty((m, n), dtype=torch.float32, device=dev) for (_, _, n, _, _) in base]
-              for _ in range(args.pool)]
+              for _ in range(nout)]
 
         def fn(i):
-            li = i % args.pool
-            for j, w in enumerate(layers[li]):
-                q.gemv(w, xs[j], ys[li][j], m=m)
+            li = i % len(lays)
+            layer_call(lays[li], xs, ys[li % nout], m)
         return fn, xs, ys
 
     step_bytes = {m: sum(wl.algorithmic_bytes(m, k, n) for _, k, n, _, _ in base) for m in (1, 2, 4, 8)}
 
     # ---- headline: M = 1 ----
-    fn, xs, ys = decode_step_fn(1)
+    fn, xs, ys = decode_step_fn(1, layers, args.pool)
     el, g = time_graph(torch, fn, steps, args.warmup, not args.eager)
     value = step_bytes[1] * steps / el / 1e9
     ms_per_step = el / steps * 1e3
@@ -236,20 +267,39 @@ def main():
         for a, b in zip(ref_out, ys[(steps - 1) % args.pool]):
             assert torch.equal(a, b), "graph replay differs from eager launch"
     log(f"M=1: {value:.1f} GB/s, {ms_per_step * 1e3:.1f} us/step ({'graph' if g is not None else 'eager'})")
-    n_launch = steps * len(base)
+    n_launch = steps * 4
     roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("gemv_fp8_kernel_decode_m1_layer.md"),
             "kernel": "gemv_fp8_kernel", "launches": n_launch,
             "avg_launch_us": round(el / n_launch * 1e6, 3),
-            "bytes_per_launch": step_bytes[1] // len(base)}
+            "bytes_per_launch": step_bytes[1] // 4}
     del g
+
+    # ---- full decode token: the whole stack back to back at M = 1 ----
+    stack_out = None
+    if args.stack_layers:
+        sfn, _, _ = decode_step_fn(1, stack, 1)
+        nl = len(stack)
+
+        def token(i):
+            for li in range(nl):
+                sfn(li)
+        reps = 3
+        el_s, gs = time_graph(torch, token, reps, 1, not args.eager)
+        tok_bytes = step_bytes[1] * nl
+        stack_out = {"layers": nl, "launches_per_token": 4 * nl, "bytes_per_token": tok_bytes,
+                     "ms_per_token": round(el_s / reps * 1e3, 4),
+                     "GBps": round(tok_bytes * reps / el_s / 1e9, 1),
+                     "frac_of_hbm_peak": round(tok_bytes * reps / el_s / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"stack: {stack_out}")
+        del gs
 
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----
     sweep = {}
     if not args.no_sweep:
         for m in (1, 2, 4, 8):
-            fn_m, xs_m, ys_m = decode_step_fn(m)
+            fn_m, xs_m, ys_m = decode_step_fn(m, layers, args.pool)
             per_shape = {}
             for j, (name, k, n, _, _) in enumerate(base):
                 def one(i, j=j):
@@ -306,12 +356,13 @@ def main():
         "dtype": "e4m3 weights x fp32 activations, fp32 accumulation",
         "data": "synthetic (seeded N(0,0.02) weights quantized per 128x128 block, N(0,1) activations)",
         "config": {"workload": "decode GEMV, M=1, one layer's projections 5120->6144, 4096->5120, "
-                               "5120->17408 x2, 17408->5120 per step",
+                               "5120->17408 x2 (gate+up as one multi4 call), 17408->5120 per step",
                    "m": 1, "pool_layers": args.pool, "bytes_per_step": step_bytes[1],
                    "launch": "hip graph" if not args.eager else "eager"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "decode_sweep": sweep or None,
+        "decode_stack": stack_out,
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)

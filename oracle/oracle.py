@@ -229,3 +229,20 @@ class RefMM:
         y = np.empty(rows, np.float32)
         self.lib.q35_mm_bf16(_p(W16, _u16p), rows, cols, _p(x, _f32p), _p(y, _f32p))
         return y
+
+    def multi4(self, Ws, scs, x) -> list:
+        """q35_mm_fp8_multi4 over up to four weights sharing x
+        (qwen35-c/src/q35_mm.c:176-198)."""
+        n = len(Ws)
+        assert 1 <= n <= 4
+        Ws = [np.ascontiguousarray(W, np.uint8) for W in Ws]
+        scs = [np.ascontiguousarray(sc, np.uint16) for sc in scs]
+        cols = Ws[0].shape[1]
+        x = np.ascontiguousarray(x, np.float32)
+        ys = [np.empty(W.shape[0], np.float32) for W in Ws]
+        wp = (_u8p * 4)(*[_p(W, _u8p) for W in Ws], *[None] * (4 - n))
+        sp = (_u16p * 4)(*[_p(sc, _u16p) for sc in scs], *[None] * (4 - n))
+        rows = (C.c_uint32 * 4)(*[W.shape[0] for W in Ws], *[0] * (4 - n))
+        yp = (_f32p * 4)(*[_p(y, _f32p) for y in ys], *[None] * (4 - n))
+        self.lib.q35_mm_fp8_multi4(wp, sp, rows, cols, _p(x, _f32p), yp)
+        return ys
