@@ -51,6 +51,9 @@ static_assert(kGemmLds <= 160 * 1024, "LDS");
 
 // One wavefront copies 1 KiB: lane l's 16 bytes at g go to LDS l*16 past l.
 // The LDS address must be the same for all lanes (it goes through M0).
+// Buffer resource word 3 for raw (untyped) buffer accesses on gfx9.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
 // s_waitcnt immediate that waits only for vmcnt <= n (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr uint32_t waitcnt_vm(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
@@ -327,19 +330,28 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     }
 
     // ---- split-K: publish, ticket, ordered sum by the last slice ----
-    // Device-scope atomic stores reach the coherence point (no L2 writeback
-    // needed to publish); the last workgroup to arrive adds the slices in
-    // order, so the result does not depend on timing.
+    // A slice's partial tile is stored in the accumulator layout: float4 q of
+    // thread t (q = (i*2 + jn)*4 + r/4) at (q*512 + t)*16 bytes, so every
+    // store and load is a coalesced 16-byte access.  They carry the sc1
+    // (device-coherent) cache policy: stores reach the coherence point, loads
+    // bypass this XCD's possibly stale L2, so publishing needs no L2 writeback.
+    // The last workgroup to arrive adds the slices in slice order (its own
+    // from registers), so the result does not depend on timing.
     constexpr uint32_t kTileElems = kGemmTile * kGemmTile;
-    float *part = p.ws + ((size_t)tile * S + sl) * kTileElems;
+    constexpr uint32_t kQuads = 32;                     // float4s per thread
+    constexpr int kCoherent = 16;                       // sc1
+    const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(
+        p.ws + (size_t)tile * S * kTileElems, 0, S * kTileElems * 4, kBufferRsrcWord3);
+    auto quad_off = [&](uint32_t s2, uint32_t q) -> int {
+        return (int)((s2 * kTileElems + (q * kGemmThreads + threadIdx.x) * 4) * 4);
+    };
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-        for (uint32_t jn = 0; jn < 2; jn++)
-#pragma unroll
-            for (uint32_t r = 0; r < 16; r++)
-                __hip_atomic_store(part + out_row(i, r) * kGemmTile + out_col(jn), acc[i][jn][r], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t q = 0; q < kQuads; q++) {
+        const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
+        const u32x4_t v = {f32_bits(acc[i][jn][4 * r4]), f32_bits(acc[i][jn][4 * r4 + 1]),
+                           f32_bits(acc[i][jn][4 * r4 + 2]), f32_bits(acc[i][jn][4 * r4 + 3])};
+        __builtin_amdgcn_raw_buffer_store_b128(v, part, quad_off(sl, q), 0, kCoherent);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t *ticket = reinterpret_cast<uint32_t *>(lds + kTicketOff);
@@ -348,22 +360,42 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     __syncthreads();
     if (*ticket != S - 1) return;
 
-    const float *base = p.ws + (size_t)tile * S * kTileElems;
-    for (uint32_t e = threadIdx.x * 4; e < kTileElems; e += kGemmThreads * 4) {
-        float sum[4];
+    // Ordered sum tot = ((p_0 + p_1) + p_2) + ..., all slices read back (this
+    // workgroup's too, so its accumulators are free), eight float4s of each
+    // of up to four slices in flight at a time.
+    constexpr uint32_t kGroupQuads = 8;
+    constexpr uint32_t kBatch = 4;
 #pragma unroll
-        for (uint32_t u = 0; u < 4; u++)
-            sum[u] = __hip_atomic_load(base + e + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (uint32_t s2 = 1; s2 < S; s2++)
+    for (uint32_t g = 0; g < kQuads / kGroupQuads; g++) {
+        u32x4_t tot[kGroupQuads];
+        for (uint32_t s0 = 0; s0 < S; s0 += kBatch) {
+            u32x4_t v[kBatch][kGroupQuads];
 #pragma unroll
-            for (uint32_t u = 0; u < 4; u++)
-                sum[u] += __hip_atomic_load(base + (size_t)s2 * kTileElems + e + u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t mrow = mt * kGemmTile + e / kGemmTile;
+            for (uint32_t b = 0; b < kBatch; b++)
 #pragma unroll
-        for (uint32_t u = 0; u < 4; u++) {
-            const uint32_t ncol = nt * kGemmTile + (e + u) % kGemmTile;
-            if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = sum[u];
+                for (uint32_t q = 0; q < kGroupQuads; q++)
+                    v[b][q] = __builtin_amdgcn_raw_buffer_load_b128(part, quad_off(min(s0 + b, S - 1), g * kGroupQuads + q),
+                                                                    0, kCoherent);
+#pragma unroll
+            for (uint32_t b = 0; b < kBatch; b++) {
+                if (s0 + b >= S) break;
+#pragma unroll
+                for (uint32_t q = 0; q < kGroupQuads; q++)
+#pragma unroll
+                    for (uint32_t e = 0; e < 4; e++)
+                        tot[q][e] = s0 + b == 0 ? v[b][q][e] : f32_bits(bits_f32(tot[q][e]) + bits_f32(v[b][q][e]));
+            }
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kGroupQuads; q++) {
+            const uint32_t qq = g * kGroupQuads + q;
+            const uint32_t i = qq >> 3, jn = (qq >> 2) & 1, r4 = qq & 3;
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) {
+                const uint32_t mrow = mt * kGemmTile + out_row(i, 4 * r4 + e);
+                const uint32_t ncol = nt * kGemmTile + out_col(jn);
+                if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = bits_f32(tot[q][e]);
+            }
         }
     }
     if (threadIdx.x == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
