@@ -23,8 +23,11 @@
 //    v_mul per accumulator and K block, and the scale is never folded into
 //    bf16 weights (that would round).  A block with scale 0 contributes
 //    nothing and is skipped.
-//  - Split-K with a deterministic last-arriver fixup when output tiles alone
-//    cannot occupy the device.
+//  - Work split: whole rounds of tiles unsplit, the tiles of a last partial
+//    round cut along K; their partial tiles are added in slice order by a
+//    second kernel (deterministic, spread over the whole device).
+#include <algorithm>
+
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
 
@@ -39,8 +42,7 @@ constexpr uint32_t kStageA = kGemmTile * kStageK * 2;     // 32 KiB bf16
 constexpr uint32_t kStageB = kGemmTile * kStageK;         // 16 KiB e4m3
 constexpr uint32_t kStageBytes = kStageA + kStageB;       // 48 KiB
 constexpr uint32_t kRing = 3;
-constexpr uint32_t kTicketOff = kRing * kStageBytes;      // 144 KiB
-constexpr uint32_t kScaleOff = kTicketOff + 64;           // [2][kGemmMaxSliceKb] fp32
+constexpr uint32_t kScaleOff = kRing * kStageBytes;       // 144 KiB: [2][kGemmMaxSliceKb] fp32
 constexpr uint32_t kGemmLds = kScaleOff + 2 * kGemmMaxSliceKb * 4;
 constexpr uint32_t kALoads = 4;    // 1 KiB pieces of A per wavefront per stage
 constexpr uint32_t kBLoads = 2;    // 1 KiB pieces of B per wavefront per stage
@@ -51,9 +53,6 @@ static_assert(kGemmLds <= 160 * 1024, "LDS");
 
 // One wavefront copies 1 KiB: lane l's 16 bytes at g go to LDS l*16 past l.
 // The LDS address must be the same for all lanes (it goes through M0).
-// Buffer resource word 3 for raw (untyped) buffer accesses on gfx9.
-constexpr int kBufferRsrcWord3 = 0x00020000;
-
 // s_waitcnt immediate that waits only for vmcnt <= n (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr uint32_t waitcnt_vm(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
@@ -121,9 +120,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     lds_u8 *const ring = (lds_u8 *)lds;
 
-    const uint32_t S = p.nslices;
-    const uint32_t tile = blockIdx.x / S;
-    const uint32_t sl = blockIdx.x - tile * S;
+    const bool split = blockIdx.x >= p.split_tile0;
+    const uint32_t S = split ? p.nslices : 1;
+    const uint32_t u = split ? blockIdx.x - p.split_tile0 : 0;
+    const uint32_t tile = split ? p.split_tile0 + u / S : blockIdx.x;
+    const uint32_t sl = split ? u % S : 0;
     const uint32_t mt = tile % p.mtiles;
     const uint32_t nt = tile / p.mtiles;
     const uint32_t KB = p.kb;
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     };
     auto out_col = [&](uint32_t jn) -> uint32_t { return wn * 64 + jn * 32 + (lane & 31); };
 
-    if (S == 1) {
+    if (!split) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++)
 #pragma unroll
@@ -329,87 +330,82 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         return;
     }
 
-    // ---- split-K: publish, ticket, ordered sum by the last slice ----
-    // A slice's partial tile is stored in the accumulator layout: float4 q of
-    // thread t (q = (i*2 + jn)*4 + r/4) at (q*512 + t)*16 bytes, so every
-    // store and load is a coalesced 16-byte access.  They carry the sc1
-    // (device-coherent) cache policy: stores reach the coherence point, loads
-    // bypass this XCD's possibly stale L2, so publishing needs no L2 writeback.
-    // The last workgroup to arrive adds the slices in slice order (its own
-    // from registers), so the result does not depend on timing.
-    constexpr uint32_t kTileElems = kGemmTile * kGemmTile;
-    constexpr uint32_t kQuads = 32;                     // float4s per thread
-    constexpr int kCoherent = 16;                       // sc1
-    const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(
-        p.ws + (size_t)tile * S * kTileElems, 0, S * kTileElems * 4, kBufferRsrcWord3);
-    auto quad_off = [&](uint32_t s2, uint32_t q) -> int {
-        return (int)((s2 * kTileElems + (q * kGemmThreads + threadIdx.x) * 4) * 4);
-    };
+    // ---- split tile: publish this slice's partial ----
+    // Stored in the accumulator layout, float4 q of thread t (q = (i*2 + jn)*4
+    // + r/4) at (q*512 + t)*16 bytes of the slice's 256 KiB, so every store is
+    // a coalesced 16-byte access; gemm_reduce maps it back to (row, column).
+    const size_t slot = (size_t)(tile - p.split_tile0) * S + sl;
+    float4 *part = reinterpret_cast<float4 *>(p.ws + slot * kGemmTile * kGemmTile);
 #pragma unroll
-    for (uint32_t q = 0; q < kQuads; q++) {
+    for (uint32_t q = 0; q < 32; q++) {
         const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
-        const u32x4_t v = {f32_bits(acc[i][jn][4 * r4]), f32_bits(acc[i][jn][4 * r4 + 1]),
-                           f32_bits(acc[i][jn][4 * r4 + 2]), f32_bits(acc[i][jn][4 * r4 + 3])};
-        __builtin_amdgcn_raw_buffer_store_b128(v, part, quad_off(sl, q), 0, kCoherent);
+        part[q * kGemmThreads + threadIdx.x] =
+            make_float4(acc[i][jn][4 * r4], acc[i][jn][4 * r4 + 1], acc[i][jn][4 * r4 + 2], acc[i][jn][4 * r4 + 3]);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t *ticket = reinterpret_cast<uint32_t *>(lds + kTicketOff);
-    if (threadIdx.x == 0)
-        *ticket = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (*ticket != S - 1) return;
-
-    // Ordered sum tot = ((p_0 + p_1) + p_2) + ..., all slices read back (this
-    // workgroup's too, so its accumulators are free), eight float4s of each
-    // of up to four slices in flight at a time.
-    constexpr uint32_t kGroupQuads = 8;
-    constexpr uint32_t kBatch = 4;
-#pragma unroll
-    for (uint32_t g = 0; g < kQuads / kGroupQuads; g++) {
-        u32x4_t tot[kGroupQuads];
-        for (uint32_t s0 = 0; s0 < S; s0 += kBatch) {
-            u32x4_t v[kBatch][kGroupQuads];
-#pragma unroll
-            for (uint32_t b = 0; b < kBatch; b++)
-#pragma unroll
-                for (uint32_t q = 0; q < kGroupQuads; q++)
-                    v[b][q] = __builtin_amdgcn_raw_buffer_load_b128(part, quad_off(min(s0 + b, S - 1), g * kGroupQuads + q),
-                                                                    0, kCoherent);
-#pragma unroll
-            for (uint32_t b = 0; b < kBatch; b++) {
-                if (s0 + b >= S) break;
-#pragma unroll
-                for (uint32_t q = 0; q < kGroupQuads; q++)
-#pragma unroll
-                    for (uint32_t e = 0; e < 4; e++)
-                        tot[q][e] = s0 + b == 0 ? v[b][q][e] : f32_bits(bits_f32(tot[q][e]) + bits_f32(v[b][q][e]));
-            }
-        }
-#pragma unroll
-        for (uint32_t q = 0; q < kGroupQuads; q++) {
-            const uint32_t qq = g * kGroupQuads + q;
-            const uint32_t i = qq >> 3, jn = (qq >> 2) & 1, r4 = qq & 3;
-#pragma unroll
-            for (uint32_t e = 0; e < 4; e++) {
-                const uint32_t mrow = mt * kGemmTile + out_row(i, 4 * r4 + e);
-                const uint32_t ncol = nt * kGemmTile + out_col(jn);
-                if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = bits_f32(tot[q][e]);
-            }
-        }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-uint32_t gemm_slices(uint32_t mtiles, uint32_t ntiles, uint32_t kb) {
-    // Split K only when the output tiles cannot occupy a 256-CU device; each
-    // slice keeps at least four K blocks and at most kGemmMaxSliceKb (the
-    // slice's scales are staged in LDS).
-    const uint32_t tiles = mtiles * ntiles;
-    uint32_t s = 1;
-    while (tiles * (s + 1) <= 256 && (s + 1) * 4 <= kb) s++;
-    while ((kb + s - 1) / s > kGemmMaxSliceKb) s++;
-    return s;
+// Ordered sum of the K slices of split tiles: y = ((p_0 + p_1) + p_2) + ...
+// One thread per float4 of a partial tile (16384 per tile); the layout is
+// the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
+// the partials are visible without any device-scope protocol.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+    constexpr uint32_t kTileQuads = kGemmTile * kGemmTile / 4;
+    const uint32_t f = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t st = f / kTileQuads;                 // split tile index
+    const uint32_t fq = f - st * kTileQuads;
+    const uint32_t tile = p.split_tile0 + st;
+    const uint32_t S = p.nslices;
+    const float4 *part = reinterpret_cast<const float4 *>(p.ws) + (size_t)st * S * kTileQuads + fq;
+    float4 v[8];
+    float4 tot = part[0];
+    for (uint32_t s0 = 1; s0 < S; s0 += 8) {
+#pragma unroll
+        for (uint32_t b = 0; b < 8; b++) v[b] = part[(size_t)min(s0 + b, S - 1) * kTileQuads];
+#pragma unroll
+        for (uint32_t b = 0; b < 8; b++)
+            if (s0 + b < S) {
+                tot.x += v[b].x;
+                tot.y += v[b].y;
+                tot.z += v[b].z;
+                tot.w += v[b].w;
+            }
+    }
+    // accumulator layout -> output coordinates (as out_row / out_col)
+    const uint32_t t = fq % kGemmThreads, q = fq / kGemmThreads;
+    const uint32_t lane = t & 63, wv = t >> 6, wm = wv & 1, wn = wv >> 1;
+    const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
+    const uint32_t mt = tile % p.mtiles, nt = tile / p.mtiles;
+    const uint32_t row0 = mt * kGemmTile + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+    const uint32_t col = nt * kGemmTile + wn * 64 + jn * 32 + (lane & 31);
+    const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
+    if (col < p.rows) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4; e++)
+            if (row0 + e < p.m) p.y[(size_t)(row0 + e) * p.ldy + col] = tv[e];
+    }
+}
+
+GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
+    // Whole rounds of tiles run unsplit; the tiles of the last, partial round
+    // are cut along K so that round fills the device too.  A slice keeps at
+    // least two K blocks (four pipeline stages).  A K range longer than the
+    // LDS scale table (kGemmMaxSliceKb blocks) splits every tile.
+    GemmPlan pl{};
+    pl.mtiles = (m + kGemmTile - 1) / kGemmTile;
+    pl.ntiles = (nb + 1) / 2;
+    const uint32_t tiles = pl.mtiles * pl.ntiles;
+    const uint32_t smin = (kb + kGemmMaxSliceKb - 1) / kGemmMaxSliceKb;
+    if (smin > 1) {
+        pl.split_tile0 = 0;
+        pl.nslices = smin;
+        return pl;
+    }
+    const uint32_t whole = tiles / cus * cus;
+    const uint32_t rest = tiles - whole;
+    const uint32_t s = rest ? std::min(cus / rest, std::max(1u, kb / 2)) : 1;
+    pl.split_tile0 = s > 1 ? whole : tiles;
+    pl.nslices = s > 1 ? s : 1;
+    return pl;
 }
 
 hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k, uint32_t m32_tiles,
@@ -426,8 +422,13 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const uint32_t grid = p.mtiles * p.ntiles * p.nslices;
+    const uint32_t tiles = p.mtiles * p.ntiles;
+    const uint32_t grid = p.split_tile0 + (tiles - p.split_tile0) * p.nslices;
     hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
+    if (p.split_tile0 < tiles) {
+        const uint32_t quads = (tiles - p.split_tile0) * (kGemmTile * kGemmTile / 4);
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3(quads / 256), dim3(256), 0, stream, p);
+    }
     return hipGetLastError();
 }
 

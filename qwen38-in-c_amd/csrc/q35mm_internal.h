@@ -82,13 +82,19 @@ constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
 constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64
 constexpr uint32_t kGemmMaxSliceKb = 1024;  // K blocks one workgroup may cover
 
+// Work split.  Tiles (mt, nt) are numbered tile = nt * mtiles + mt.  Tiles
+// below split_tile0 are whole (one workgroup, written straight to y); the
+// rest are cut into nslices K slices each, whose partial tiles go to ws and
+// are added in slice order by gemm_reduce.  Workgroup b < split_tile0 owns
+// tile b; workgroup split_tile0 + u owns slice u % nslices of tile
+// split_tile0 + u / nslices.  With whole tiles first, the split workgroups
+// fill the CUs the last round of whole tiles leaves idle.
 struct GemmParams {
     const uint16_t *xb;  // lane-order bf16 activations, mtiles*256 rows
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
-    float *ws;
-    uint32_t *cnt;
+    float *ws;           // partial tiles of split tiles, 256 KiB each
     uint32_t m;
     uint32_t rows;
     uint32_t ldy;
@@ -96,16 +102,22 @@ struct GemmParams {
     uint32_t nb;         // 128-row groups of the weight
     uint32_t mtiles;
     uint32_t ntiles;
-    uint32_t nslices;
+    uint32_t split_tile0;
+    uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
 };
 
-uint32_t gemm_slices(uint32_t mtiles, uint32_t ntiles, uint32_t kb);
+struct GemmPlan {
+    uint32_t mtiles, ntiles, split_tile0, nslices;
+    uint32_t grid() const { return split_tile0 + (mtiles * ntiles - split_tile0) * nslices; }
+    size_t ws_bytes() const { return (size_t)(mtiles * ntiles - split_tile0) * nslices * kGemmTile * kGemmTile * 4; }
+};
+GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus);
 // X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
 // multiple of 32 (m32 tiles = rows_pad / 32).
 hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
                               uint32_t m32_tiles, uint32_t kb, uint16_t *xb,
                               hipStream_t stream);
-hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);   // + gemm_reduce when split
 
 // ---- residency / conversions -----------------------------------------
 // Row-major raw codes (device) -> lane-order tiles (device).

@@ -282,33 +282,30 @@ int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hip
     const Weight &w = wt->w;
     if (!gemm_fits(w, m))
         return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
-    const uint32_t mtiles = (m + kGemmTile - 1) / kGemmTile;
-    const uint32_t ntiles = (w.nb + 1) / 2;   // 256 output columns = two 128-row groups
-    const size_t xb_bytes = (size_t)mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
+    const GemmPlan pl = gemm_plan(m, w.nb, w.kb, g_dev.cus);
+    const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
     int rc = grow(g_dev.xb, xb_bytes, false);
     if (rc) return rc;
+    if (pl.ws_bytes()) {
+        rc = grow(g_dev.ws, pl.ws_bytes(), false);
+        if (rc) return rc;
+    }
     GemmParams p{};
     p.xb = (const uint16_t *)g_dev.xb.ptr;
     p.codes = w.codes;
     p.scale = w.scale;
     p.y = dY;
+    p.ws = (float *)g_dev.ws.ptr;
     p.m = m;
     p.rows = w.rows;
     p.ldy = w.rows;
     p.kb = w.kb;
     p.nb = w.nb;
-    p.mtiles = mtiles;
-    p.ntiles = ntiles;
-    p.nslices = gemm_slices(mtiles, ntiles, w.kb);
-    const size_t tiles = (size_t)mtiles * ntiles;
-    if (p.nslices > 1) {
-        rc = grow(g_dev.ws, tiles * p.nslices * kGemmTile * kGemmTile * sizeof(float), false);
-        if (rc) return rc;
-    }
-    rc = grow(g_dev.cnt, tiles * sizeof(uint32_t), true);
-    if (rc) return rc;
-    p.ws = (float *)g_dev.ws.ptr;
-    p.cnt = (uint32_t *)g_dev.cnt.ptr;
+    p.mtiles = pl.mtiles;
+    p.ntiles = pl.ntiles;
+    p.split_tile0 = pl.split_tile0;
+    p.nslices = pl.nslices;
+    const uint32_t mtiles = pl.mtiles;
     HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles * (kGemmTile / kSubRows), w.kb, (uint16_t *)g_dev.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
