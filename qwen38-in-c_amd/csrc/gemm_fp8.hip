@@ -325,7 +325,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
                 for (uint32_t r = 0; r < 16; r++) {
                     const uint32_t mrow = mt * kGemmTile + out_row(i, r);
                     const uint32_t ncol = nt * kGemmTile + out_col(jn);
-                    if (mrow < p.m && ncol < p.rows) p.y[(size_t)mrow * p.ldy + ncol] = acc[i][jn][r];
+                    if (mrow < p.m && ncol < p.rows)
+                        __builtin_nontemporal_store(acc[i][jn][r], p.y + (size_t)mrow * p.ldy + ncol);
                 }
         return;
     }
