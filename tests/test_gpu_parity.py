@@ -240,6 +240,47 @@ def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
 
 
+def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
+    """Blocks whose scale is 0 contribute nothing (the reference's
+    lut[code] * 0): first K blocks of a row group, blocks in the middle and a
+    whole row group, with nonzero codes behind them.  A row group with no
+    live block must come out exactly 0."""
+    import torch
+    m, k, n = 96, 1536, 640
+    rng = np.random.default_rng(91)
+    W = rng.integers(0, 0x7E, size=(n, k), dtype=np.uint8) | (rng.integers(0, 2, size=(n, k), dtype=np.uint8) << 7)
+    sc = np.full((n // 128, k // 128), 0x3980, np.uint16)           # bf16 2^-12: outputs of unit scale
+    sc[0, 0] = 0                      # first block of group 0
+    sc[1, 5:7] = 0                    # middle blocks of group 1
+    sc[2, :] = 0                      # group 2 dead
+    sc[3, -1] = 0                     # last block of group 3
+    X = wl.gen_act(92, m, k)
+    w = q.Weight(W, sc)
+    dY = torch.empty((m, n), dtype=torch.float32, device=gpu)
+    q.gemm(w, _torch_dev(X, gpu), dY)
+    torch.cuda.synchronize()
+    Y = dY.cpu().numpy()
+    Yr = oracle.mm_batch(W, sc, X)
+    rel, mx = _gemm_check(Y, Yr)
+    assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
+    assert (Y[:, 256:384] == 0).all()
+
+
+def test_gemm_k_beyond_one_slice_table(q, oracle, wl, gpu):
+    """K of 1025 blocks: more than one workgroup's LDS scale table, so every
+    tile is cut into two K slices and summed by the reduction kernel."""
+    import torch
+    m, k, n = 64, 1025 * 128, 256
+    W, sc = wl.gen_weight(93, n, k)
+    X = wl.gen_act(94, m, k, bf16=True)
+    w = q.Weight(W, sc)
+    dY = torch.empty((m, n), dtype=torch.float32, device=gpu)
+    q.gemm(w, _torch_dev(X, gpu), dY)
+    torch.cuda.synchronize()
+    rel, mx = _gemm_check(dY.cpu().numpy(), oracle.mm_batch(W, sc, X))
+    assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
+
+
 def test_gemm_bf16_exact_inputs_near_exact(q, oracle, wl, gpu):
     """With bf16-representable activations the only rounding left in the GEMM
     is fp32 accumulation, so it agrees with the oracle far inside the bar."""
