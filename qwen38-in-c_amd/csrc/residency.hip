@@ -140,38 +140,112 @@ hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream
 // loads (8 bf16) strided by 1 KiB and the wavefront reduces with a
 // butterfly of cross-lane adds.
 // ---------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bf16_gemv_kernel(const uint16_t *__restrict__ w, uint32_t rows,
-                                                        uint32_t cols, const float *__restrict__ x,
-                                                        float *__restrict__ y) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const uint16_t *wr = w + (size_t)row * cols;
-    float acc = 0.0f;
-    const bool aligned = ((cols & 7u) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15u) == 0);
-    uint32_t c = lane * 8;
-    if (aligned) {
-        for (; c + 8 <= cols; c += 512) {
-            const u32x4_t q = *reinterpret_cast<const u32x4_t *>(wr + c);
+// ---- BF16 matvec (q35_mm_bf16) ----------------------------------------
+// The reference's order exactly (qwen35-c/src/q35_mm.c:211-246): for each
+// row, eight fmaf chains acc[n % 8] over the columns in increasing order,
+// then y = ((0 + acc[0]) + acc[1]) + ... + acc[7].  One lane per row holds
+// the eight chains (independent, so the FMAs pipeline), so the result is the
+// reference's bit for bit.
+//
+// Vector path (cols % 8 == 0, W 16-byte aligned): a wavefront owns 64 rows
+// and walks K in tiles of 64 columns.  A tile (64 rows x 128 bytes) is read
+// with coalesced 16-byte loads (8 rows x 128 contiguous bytes per
+// instruction), kD tiles ahead in registers, and passed through LDS
+// (row stride 144 bytes: conflict-free 16-byte reads) so that each lane gets
+// its own row; the tile's 64 activations are broadcast from LDS.  Columns
+// >= cols are zeroed (a zero product leaves every chain unchanged).
+namespace {
+constexpr uint32_t kBf16Tile = 64;                 // columns per tile
+constexpr uint32_t kBf16Stride = 144;              // LDS bytes per row
+constexpr uint32_t kBf16WaveLds = kBf16Tile * kBf16Stride + kBf16Tile * 4;
+constexpr uint32_t kBf16Depth = 3;                 // tiles in flight per wavefront
+}  // namespace
+
+__global__ __launch_bounds__(256) void bf16_gemv_vec_kernel(const uint16_t *__restrict__ w, uint32_t rows,
+                                                            uint32_t cols, const float *__restrict__ x,
+                                                            float *__restrict__ y) {
+    __shared__ __align__(16) uint8_t lds[4 * kBf16WaveLds];
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint8_t *const tl = lds + wv * kBf16WaveLds;          // this wavefront's tile
+    float *const xl = reinterpret_cast<float *>(tl + kBf16Tile * kBf16Stride);
+    const uint32_t r0 = (blockIdx.x * 4 + wv) * 64;
+    const uint32_t ntiles = (cols + kBf16Tile - 1) / kBf16Tile;
+    const uint32_t lr = lane >> 3, lc = lane & 7;         // load role: row lr + 8i, 16-byte chunk lc
+
+    u32x4_t wt[kBf16Depth][8];
+    float xt[kBf16Depth];
+    auto load = [&](uint32_t slot, uint32_t t) {
+        const uint32_t col = min(t * kBf16Tile + lc * 8, cols - 8);   // in bounds; masked later
 #pragma unroll
-            for (int d = 0; d < 4; d++) {
-                acc = __builtin_fmaf(bits_f32(q[d] << 16), x[c + 2 * d], acc);
-                acc = __builtin_fmaf(bits_f32(q[d] & 0xFFFF0000u), x[c + 2 * d + 1], acc);
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t row = min(r0 + lr + 8 * i, rows - 1);
+            wt[slot][i] = *reinterpret_cast<const u32x4_t *>(w + (size_t)row * cols + col);
+        }
+        xt[slot] = x[min(t * kBf16Tile + lane, cols - 1)];
+    };
+#pragma unroll
+    for (uint32_t d = 0; d + 1 < kBf16Depth; d++) load(d, min(d, ntiles - 1));
+
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t t0 = 0; t0 < ntiles; t0 += kBf16Depth) {
+#pragma unroll
+        for (uint32_t d = 0; d < kBf16Depth; d++) {
+            const uint32_t t = t0 + d;
+            load((d + kBf16Depth - 1) % kBf16Depth, min(t + kBf16Depth - 1, ntiles - 1));
+            if (t < ntiles) {
+                const bool wlive = t * kBf16Tile + lc * 8 < cols;
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++) {
+                    const u32x4_t v = wlive ? wt[d][i] : u32x4_t{0u, 0u, 0u, 0u};
+                    *reinterpret_cast<u32x4_t *>(tl + (lr + 8 * i) * kBf16Stride + lc * 16) = v;
+                }
+                xl[lane] = t * kBf16Tile + lane < cols ? xt[d] : 0.0f;
+                // Same wavefront: LDS operations complete in order.
+#pragma unroll
+                for (uint32_t c = 0; c < 8; c++) {
+                    const u32x4_t q = *reinterpret_cast<const u32x4_t *>(tl + lane * kBf16Stride + c * 16);
+                    const float4 xa = reinterpret_cast<const float4 *>(xl)[2 * c];
+                    const float4 xb = reinterpret_cast<const float4 *>(xl)[2 * c + 1];
+                    const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                    for (uint32_t e = 0; e < 4; e++) {
+                        acc[2 * e] = __builtin_fmaf(bits_f32(q[e] << 16), xv[2 * e], acc[2 * e]);
+                        acc[2 * e + 1] = __builtin_fmaf(bits_f32(q[e] & 0xFFFF0000u), xv[2 * e + 1], acc[2 * e + 1]);
+                    }
+                }
             }
         }
-    } else {
-        for (; c < cols; c += 512)
-            for (uint32_t e = 0; e < 8 && c + e < cols; e++)
-                acc = __builtin_fmaf(bits_f32((uint32_t)wr[c + e] << 16), x[c + e], acc);
     }
+    const uint32_t row = r0 + lane;
+    if (row < rows) {
+        float sum = 0.0f;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) y[row] = acc;
+        for (uint32_t j = 0; j < 8; j++) sum += acc[j];
+        y[row] = sum;
+    }
+}
+
+// Any cols / alignment: one thread per row, same order, element loads.
+__global__ __launch_bounds__(256) void bf16_gemv_any_kernel(const uint16_t *__restrict__ w, uint32_t rows,
+                                                            uint32_t cols, const float *__restrict__ x,
+                                                            float *__restrict__ y) {
+    const uint32_t row = blockIdx.x * 256 + threadIdx.x;
+    if (row >= rows) return;
+    const uint16_t *wr = w + (size_t)row * cols;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c = 0; c < cols; c++) acc[c & 7] = __builtin_fmaf(bits_f32((uint32_t)wr[c] << 16), x[c], acc[c & 7]);
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) sum += acc[j];
+    y[row] = sum;
 }
 
 hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols, const float *x, float *y,
                             hipStream_t stream) {
-    hipLaunchKernelGGL(bf16_gemv_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, w, rows, cols, x, y);
+    if (cols % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0)
+        hipLaunchKernelGGL(bf16_gemv_vec_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, w, rows, cols, x, y);
+    else
+        hipLaunchKernelGGL(bf16_gemv_any_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, w, rows, cols, x, y);
     return hipGetLastError();
 }
 
