@@ -17,7 +17,8 @@ every copy is distinct data of the same distribution.
 
 Also the full decode-token weight stream: a stack of 64 such layers (20.5 GB
 of distinct FP8 weights resident) run back to back at M=1, 256 launches per
-token (--stack-layers, 0 to skip).
+token (--stack-layers, 0 to skip), and the BF16 lm_head matvec (q35_mm_bf16,
+248320 x 5120, two resident copies alternated).
 
 value = algorithmic bytes of K steps / elapsed seconds (HIP events on the
 launch stream, launches replayed from a HIP graph), in GB/s.  Algorithmic
@@ -190,6 +191,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-lm-head", dest="lm_head", action="store_false",
+                    help="skip the BF16 lm_head matvec (248320 x 5120)")
     ap.add_argument("--stack-layers", type=int, default=64,
                     help="distinct layers of the full-token weight stream (0: skip)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -340,6 +343,29 @@ def main():
         prefill["total"] = {"TFLOPs": round(tf_all, 1), "frac_of_bf16_peak": round(tf_all / BF16_PEAK_TFLOPS, 4),
                             "note": "includes the fp32->bf16 activation prepass kernel of each call"}
 
+    # ---- BF16 lm_head matvec (q35_mm_bf16): 248320 x 5120 ----
+    lm_head = None
+    if args.lm_head:
+        rows, cols = 248320, 5120
+        # two distinct resident copies (2 x 2.54 GB), alternated: no cache reuse
+        gen = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 5)
+        pool2 = [(torch.randn(rows, cols, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
+                 for _ in range(2)]
+        xh = torch.randn(cols, device=dev, generator=gen)
+        yh = torch.empty(rows, dtype=torch.float32, device=dev)
+
+        def lm_call(i):
+            q.bf16_gemv(pool2[i % 2], xh, yh)
+        reps = 20
+        el_h, gh = time_graph(torch, lm_call, reps, 2, not args.eager)
+        lm_bytes = rows * cols * 2 + cols * 4 + rows * 4
+        lm_head = {"rows": rows, "cols": cols, "us": round(el_h / reps * 1e6, 1),
+                   "GBps": round(lm_bytes * reps / el_h / 1e9, 1),
+                   "frac_of_hbm_peak": round(lm_bytes * reps / el_h / 1e9 / HBM_PEAK_GBS, 4),
+                   "numerics": "bit-identical to the reference's q35_mm_bf16 order"}
+        log(f"lm_head: {lm_head}")
+        del gh, pool2
+
     cpu = None if args.no_cpu else cpu_baseline(wl, base)
 
     out = {
@@ -364,6 +390,7 @@ def main():
         "decode_sweep": sweep or None,
         "decode_stack": stack_out,
         "prefill": prefill,
+        "lm_head_bf16": lm_head,
     }
     print(json.dumps(out), flush=True)
 
