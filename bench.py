@@ -17,8 +17,9 @@ every copy is distinct data of the same distribution.
 
 Also the full decode-token weight stream: a stack of 64 such layers (20.5 GB
 of distinct FP8 weights resident) run back to back at M=1, 256 launches per
-token (--stack-layers, 0 to skip), and the BF16 lm_head matvec (q35_mm_bf16,
-248320 x 5120, two resident copies alternated).
+token (--stack-layers, 0 to skip), the BF16 lm_head matvec (q35_mm_bf16,
+248320 x 5120, two resident copies alternated), and one MLP block at M=1
+(RMSNorm, gate+up, SwiGLU, down, residual add on device).
 
 value = algorithmic bytes of K steps / elapsed seconds (HIP events on the
 launch stream, launches replayed from a HIP graph), in GB/s.  Algorithmic
@@ -191,6 +192,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-mlp", dest="mlp", action="store_false",
+                    help="skip the MLP block (RMSNorm, gate/up, SwiGLU, down, residual) at M=1")
     ap.add_argument("--no-lm-head", dest="lm_head", action="store_false",
                     help="skip the BF16 lm_head matvec (248320 x 5120)")
     ap.add_argument("--stack-layers", type=int, default=64,
@@ -298,6 +301,41 @@ def main():
         log(f"stack: {stack_out}")
         del gs
 
+    # ---- MLP block at M = 1: RMSNorm -> gate/up -> SwiGLU -> down -> residual ----
+    mlp_out = None
+    if args.mlp:
+        H, I = base[GATE][1], base[GATE][2]
+        gen = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
+        nws = [torch.randn(H, device=dev, generator=gen) * 0.1 for _ in range(args.pool)]
+        xres = torch.randn((1, H), device=dev, generator=gen)
+        xn = torch.randn((1, H), device=dev, generator=gen)
+        gu = [torch.empty((1, I), device=dev) for _ in range(2)]
+        yd = torch.empty((1, H), device=dev)
+
+        def block(i):
+            L = layers[i % args.pool]
+            q.mlp(L[GATE], L[UP], L[4], nws[i % args.pool], xres)
+
+        def matmuls(i):
+            L = layers[i % args.pool]
+            q.matmul_multi([L[GATE], L[UP]], xn, gu)
+            q.gemv(L[4], gu[0], yd)
+        blk_bytes = sum(wl.algorithmic_bytes(1, k, n) for _, k, n, _, _ in base[GATE:])
+        el_b, gb = time_graph(torch, block, steps, 2, not args.eager)
+        del gb
+        el_m, gm = time_graph(torch, matmuls, steps, 2, not args.eager)
+        del gm
+        mlp_out = {"m": 1, "H": H, "I": I, "bytes_per_block": blk_bytes,
+                   "us_per_block": round(el_b / steps * 1e6, 2),
+                   "GBps": round(blk_bytes * steps / el_b / 1e9, 1),
+                   "frac_of_hbm_peak": round(blk_bytes * steps / el_b / 1e9 / HBM_PEAK_GBS, 4),
+                   "us_matmuls_only": round(el_m / steps * 1e6, 2),
+                   "launches_per_block": 2,
+                   "note": "q35mm_mlp at M=1: RMSNorm (exact eight-lane order) inside the gate+up GEMV, "
+                           "SwiGLU and the residual add inside the down GEMV; us_matmuls_only = the same "
+                           "two GEMV launches on ready activations"}
+        log(f"mlp block: {mlp_out}")
+
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----
     sweep = {}
     if not args.no_sweep:
@@ -391,6 +429,7 @@ def main():
         "decode_stack": stack_out,
         "prefill": prefill,
         "lm_head_bf16": lm_head,
+        "mlp_block": mlp_out,
     }
     print(json.dumps(out), flush=True)
 

@@ -89,6 +89,33 @@ int q35mm_decode_bf16(const q35mm_weight *w, uint16_t *dOut, void *stream);
 int q35mm_bf16_gemv(const uint16_t *dW, uint32_t rows, uint32_t cols,
                     const float *dx, float *dy, void *stream);
 
+/* ---- MLP neighbours on device pointers (qwen35-c/src/q35_kern.c) ---- */
+
+/* Zero-centred RMSNorm of rows rows of n fp32: dY[r][i] = (dX[r][i] * inv_r)
+ * * (1 + dW[i]), inv_r = 1 / sqrtf(mean_r + eps), mean_r = (sum of squares in
+ * the reference's eight lanes) / n.  Bit-identical to q35_kern_rmsnorm
+ * (qwen35-c/src/q35_kern.c:88-108, sumsq_fixed :26-48) row by row.  dY may
+ * equal dX (in place, as q35_kern_qk_norm uses it). */
+int q35mm_rmsnorm(const float *dX, const float *dW, float *dY, uint32_t rows,
+                  uint32_t n, float eps, void *stream);
+/* dY[i] = (g * (1 / (1 + exp(-g)))) * dUp[i], g = dGate[i]: q35_kern_swiglu
+ * (qwen35-c/src/q35_kern.c:147-166).  exp is rounded once from double
+ * precision; libm's expf differs from that by one ulp for ~4e-5 of inputs,
+ * where dY differs from the reference by 1 to 4 ulps.  dY may equal dGate
+ * or dUp. */
+int q35mm_swiglu(const float *dGate, const float *dUp, float *dY, size_t n,
+                 void *stream);
+/* One MLP block on m tokens, in place on the residual stream dX [m][H]
+ * (H = gate cols = down rows, I = gate rows = up rows = down cols):
+ *   xn = rmsnorm(dX, dNormW, eps); g = gate(xn); u = up(xn);
+ *   dX += down(swiglu(g, u))
+ * as qwen35-c/src/q35_model.c:927-939 (one token) and :964-978 (a batch).
+ * The matmuls dispatch by m as q35mm_matmul (gate and up in one launch on
+ * the GEMV path).  Intermediates live in a library workspace. */
+int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up,
+              const q35mm_weight *down, const float *dNormW, float eps,
+              uint32_t m, float *dX, void *stream);
+
 /* Drop the resident copy that the q35_mm_* entry points made for host
  * pointer W (no-op if none).  q35mm_release_all drops every such copy. */
 void q35mm_release(const void *W);

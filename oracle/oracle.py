@@ -1,5 +1,6 @@
 """ctypes wrapper around the CPU oracle (oracle/liboracle.so) and, when built,
-the reference's own compiled matmul (oracle/_ref/libq35ref*.so).
+the reference's own compiled matmul and elementwise kernels
+(oracle/_ref/libq35ref*.so, oracle/_ref/libq35kern.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check in
 __graft_entry__.py and by the cpu_baseline leg of bench.py.  The product
@@ -17,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libq35ref.so")
 REF_SCALAR_PATH = os.path.join(HERE, "_ref", "libq35ref_scalar.so")
+REF_KERN_PATH = os.path.join(HERE, "_ref", "libq35kern.so")
 
 _u8p = C.POINTER(C.c_uint8)
 _u16p = C.POINTER(C.c_uint16)
@@ -72,6 +74,11 @@ class Oracle:
         L.orc_fnv1a32.restype = C.c_uint32
         L.orc_fnv1a32.argtypes = [C.c_void_p, C.c_size_t]
         L.orc_num_threads.restype = C.c_int
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_uint32, C.c_uint32, C.c_float]
+        L.orc_silu.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, C.c_size_t]
+        L.orc_add_inplace.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.orc_expf.argtypes = [_f32p, _f32p, C.c_size_t]
 
     # ---- decoders / quantizer ----
     def lut(self) -> np.ndarray:
@@ -154,6 +161,61 @@ class Oracle:
         y = np.empty(rows, np.float32)
         self.lib.orc_mm_bf16(_p(W16, _u16p), rows, cols, _p(x, _f32p), _p(y, _f32p))
         return y
+
+    # ---- MLP neighbours (qwen35-c/src/q35_kern.c) ----
+    def rmsnorm(self, X: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+        """Row-wise zero-centred RMSNorm of X [rows][n] (or one vector)."""
+        X = np.ascontiguousarray(X, np.float32)
+        n = X.shape[-1]
+        rows = X.size // n if n else 0
+        w = np.ascontiguousarray(w, np.float32)
+        assert w.shape == (n,)
+        Y = np.empty_like(X)
+        if X.size:
+            self.lib.orc_rmsnorm(_p(X, _f32p), _p(w, _f32p), _p(Y, _f32p), rows, n, eps)
+        return Y
+
+    def silu(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.orc_silu(_p(x, _f32p), _p(y, _f32p), x.size)
+        return y
+
+    def swiglu(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        assert g.shape == u.shape
+        y = np.empty_like(g)
+        self.lib.orc_swiglu(_p(g, _f32p), _p(u, _f32p), _p(y, _f32p), g.size)
+        return y
+
+    def add(self, x: np.ndarray, y: np.ndarray) -> np.ndarray:
+        """x + y elementwise as the residual update (returns a new array)."""
+        out = np.array(x, np.float32, copy=True, order="C")
+        y = np.ascontiguousarray(y, np.float32)
+        assert out.shape == y.shape
+        self.lib.orc_add_inplace(_p(out, _f32p), _p(y, _f32p), out.size)
+        return out
+
+    def expf(self, x: np.ndarray) -> np.ndarray:
+        """libm expf per element (what the reference's sigmoid calls)."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.orc_expf(_p(x, _f32p), _p(y, _f32p), x.size)
+        return y
+
+    def mlp(self, x: np.ndarray, norm_w: np.ndarray, gate, up, down, eps: float = 1e-6) -> np.ndarray:
+        """One MLP block on token-major x [m][H]: post-attention RMSNorm,
+        gate/up, SwiGLU, down, residual add (qwen35-c/src/q35_model.c:927-939,
+        :964-978).  gate/up/down are (codes, bf16 scale) pairs.  Returns the
+        new residual stream and the intermediates as a dict."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, norm_w.shape[0])
+        xn = self.rmsnorm(x, norm_w, eps)
+        g = self.mm_batch(gate[0], gate[1], xn)
+        u = self.mm_batch(up[0], up[1], xn)
+        mid = self.swiglu(g, u)
+        y = self.mm_batch(down[0], down[1], mid)
+        return {"xn": xn, "gate": g, "up": u, "mid": mid, "y": y, "out": self.add(x, y)}
 
     # ---- hashes ----
     def fnv64(self, a: np.ndarray) -> int:
@@ -246,3 +308,43 @@ class RefMM:
         yp = (_f32p * 4)(*[_p(y, _f32p) for y in ys], *[None] * (4 - n))
         self.lib.q35_mm_fp8_multi4(wp, sp, rows, cols, _p(x, _f32p), yp)
         return ys
+
+
+class RefKern:
+    """The reference's compiled q35_kern.c (oracle/_ref/libq35kern.so)."""
+
+    def __init__(self, path: str = REF_KERN_PATH):
+        self.lib = L = C.CDLL(path)
+        for nm in ("q35_kern_rmsnorm", "q35_kern_rmsnorm_scalar"):
+            getattr(L, nm).argtypes = [_f32p, _f32p, _f32p, C.c_size_t, C.c_float]
+        for nm in ("q35_kern_silu", "q35_kern_silu_scalar"):
+            getattr(L, nm).argtypes = [_f32p, _f32p, C.c_size_t]
+        for nm in ("q35_kern_swiglu", "q35_kern_swiglu_scalar"):
+            getattr(L, nm).argtypes = [_f32p, _f32p, _f32p, C.c_size_t]
+
+    @staticmethod
+    def available(path: str = REF_KERN_PATH) -> bool:
+        return os.path.exists(path)
+
+    def rmsnorm(self, x, w, eps=1e-6, scalar=False) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        y = np.empty_like(x)
+        fn = self.lib.q35_kern_rmsnorm_scalar if scalar else self.lib.q35_kern_rmsnorm
+        fn(_p(x, _f32p), _p(w, _f32p), _p(y, _f32p), x.size, eps)
+        return y
+
+    def silu(self, x, scalar=False) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        fn = self.lib.q35_kern_silu_scalar if scalar else self.lib.q35_kern_silu
+        fn(_p(x, _f32p), _p(y, _f32p), x.size)
+        return y
+
+    def swiglu(self, g, u, scalar=False) -> np.ndarray:
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        y = np.empty_like(g)
+        fn = self.lib.q35_kern_swiglu_scalar if scalar else self.lib.q35_kern_swiglu
+        fn(_p(g, _f32p), _p(u, _f32p), _p(y, _f32p), g.size)
+        return y

@@ -1,5 +1,6 @@
 /*
- * q35_oracle.c -- CPU restatement of the qwen35-c FP8 block-dequant matmul.
+ * q35_oracle.c -- CPU restatement of the qwen35-c FP8 block-dequant matmul
+ * and of its MLP neighbours (RMSNorm, SiLU, SwiGLU, residual add).
  *
  * TEST INFRASTRUCTURE ONLY (see q35_oracle.h).  Compiled without FP
  * contraction so every multiply and every fmaf rounds exactly as the
@@ -317,6 +318,73 @@ void orc_mm_bf16(const uint16_t *W, uint32_t rows, uint32_t cols,
         for (int j = 0; j < 8; j++) sum += acc[j];
         y[r] = sum;
     }
+}
+
+/* ------------------------------------------------------------------ */
+/* MLP neighbours (Q/src/q35_kern.c)                                    */
+/* ------------------------------------------------------------------ */
+
+/* Q/src/q35_kern.c:26-48 (sumsq_fixed) and :77-86 (q35_kern_rmsnorm_scalar).
+ * The AVX2 variants (:29-38, :88-108) run the same operations lane for lane;
+ * the reference's test checks the two paths hash-equal. */
+void orc_rmsnorm(const float *x, const float *w, float *y, uint32_t rows,
+                 uint32_t n, float eps)
+{
+    #pragma omp parallel for schedule(static) if (rows > 1)
+    for (int64_t r = 0; r < (int64_t)rows; r++) {
+        const float *xr = x + (size_t)r * n;
+        float *yr = y + (size_t)r * n;
+        float lane[8] = { 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f };
+        for (uint32_t i = 0; i < n; i++) {
+            const float sq = xr[i] * xr[i];
+            lane[i % 8u] = lane[i % 8u] + sq;
+        }
+        float s = lane[0];
+        for (int j = 1; j < 8; j++) s = s + lane[j];
+        const float mean = s / (float)n;
+        const float inv = 1.0f / sqrtf(mean + eps);
+        for (uint32_t i = 0; i < n; i++) {
+            const float t = xr[i] * inv;
+            yr[i] = t * (1.0f + w[i]);
+        }
+    }
+}
+
+/* Q/src/q35_kern.c:70-73 (sigmoidf_). */
+static float sigmoid_ref(float v)
+{
+    const float e = expf(-v);
+    return 1.0f / (1.0f + e);
+}
+
+/* Q/src/q35_kern.c:112-116 (q35_kern_silu_scalar). */
+void orc_silu(const float *x, float *y, size_t n)
+{
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; i++) y[i] = x[i] * sigmoid_ref(x[i]);
+}
+
+/* Q/src/q35_kern.c:137-145 (the AVX2 variant :147-166 computes the same
+ * t = g*sigmoid(g) per element and one multiply by up). */
+void orc_swiglu(const float *gate, const float *up, float *y, size_t n)
+{
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; i++) {
+        const float t = gate[i] * sigmoid_ref(gate[i]);
+        y[i] = t * up[i];
+    }
+}
+
+/* Q/src/q35_model.c:939 and :977 (x[j] += y[j]). */
+void orc_add_inplace(float *x, const float *y, size_t n)
+{
+    for (size_t i = 0; i < n; i++) x[i] = x[i] + y[i];
+}
+
+void orc_expf(const float *x, float *y, size_t n)
+{
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; i++) y[i] = expf(x[i]);
 }
 
 /* ------------------------------------------------------------------ */

@@ -72,6 +72,24 @@ void orc_mm_fp8_f64(const uint8_t *W, const uint16_t *scale_bf16,
 void orc_mm_bf16(const uint16_t *W, uint32_t rows, uint32_t cols,
                  const float *x, float *y);
 
+/* ---- device-resident neighbours of the MLP (Q/src/q35_kern.c) ----
+ * Same operation sequence as the reference's kernels, with FP contraction
+ * off (Q/src/q35_kern.c:8): every multiply, add and divide rounds on its own.
+ * rmsnorm: sum of squares in eight lanes (element i into lane i mod 8, in
+ * increasing i), lanes folded 0..7; mean = s/(float)n;
+ * inv = 1/sqrtf(mean + eps); y[i] = (x[i]*inv) * (1 + w[i])
+ * (Q/src/q35_kern.c:26-48, :77-86).  rows independent rows of n.
+ * silu: x * (1 / (1 + expf(-x)))                      (:70-73, :112-116)
+ * swiglu: (g * (1 / (1 + expf(-g)))) * u               (:137-145)
+ * add: x[i] = x[i] + y[i], the residual update        (Q/src/q35_model.c:939) */
+void orc_rmsnorm(const float *x, const float *w, float *y, uint32_t rows,
+                 uint32_t n, float eps);
+void orc_silu(const float *x, float *y, size_t n);
+void orc_swiglu(const float *gate, const float *up, float *y, size_t n);
+void orc_add_inplace(float *x, const float *y, size_t n);
+/* libm expf of each element (the function the reference's sigmoid calls). */
+void orc_expf(const float *x, float *y, size_t n);
+
 /* ---- hashes used by the reference tests (Q/tests/test_mm.c:19-23,
  *      Q/include/q35/q35_kern.h:77-78) ---- */
 uint64_t orc_fnv1a64(const void *p, size_t n);

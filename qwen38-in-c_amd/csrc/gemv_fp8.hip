@@ -31,6 +31,16 @@
 // one adds the partials in range order.  That order is fixed by the shape,
 // so results do not depend on timing, and P depends only on the shape, so a
 // batch of m tokens gives exactly the bits of m single-token calls.
+//
+// Fused neighbours (qwen35-c/src/q35_model.c:927-939).  The staged
+// activations can be the RMSNorm of x (kXRmsNorm: every workgroup forms the
+// sum of squares of the whole row in the reference's eight-lane order, then
+// normalises the columns it stages) or SwiGLU of two inputs (kXSwiGLU), and
+// the output can be added to a residual (y = resid + product).  Each is the
+// same arithmetic as the separate kernels in mlp.hip, so a fused launch gives
+// the bits of the unfused sequence.
+#include <algorithm>
+
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
 
@@ -71,28 +81,48 @@ __device__ __forceinline__ StageItem stage_item(uint32_t i, uint32_t per_t, uint
     return it;
 }
 
-// Raw loads of one item; the address is clamped into the row so the loads
-// are unconditional (no branch between them and the weight prologue).  The
-// caller zeroes columns >= k before use (stage_mask).  With vec (x 16-byte
-// aligned, ldx % 4 == 0, k % 8 == 0) an item is two 16-byte loads at the
-// clamped column min(kg, k - 8); otherwise eight 4-byte loads.
-__device__ __forceinline__ void stage_load(float (&xv)[8], const float *x, uint32_t ldx, uint32_t k,
-                                           const StageItem &it, bool vec) {
-    const float *xp = x + (size_t)it.t * ldx;
+// Eight consecutive columns of one row at the clamped column min(kg, k - 8)
+// (vec: two 16-byte loads; the row is 16-byte aligned and k % 8 == 0) or
+// min(kg + e, k - 1) (eight 4-byte loads).  Unconditional, so no branch sits
+// between them and the weight prologue; columns >= k are zeroed later.
+__device__ __forceinline__ void load8(float (&v)[8], const float *row, uint32_t kg, uint32_t k, bool vec) {
     if (vec) {
-        const float4 *v = reinterpret_cast<const float4 *>(xp + min(it.kg, k - 8));
-        const float4 a = v[0], b = v[1];
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        const float4 *q = reinterpret_cast<const float4 *>(row + min(kg, k - 8));
+        const float4 a = q[0], b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; e++) xv[e] = xp[min(it.kg + e, k - 1)];
+        for (int e = 0; e < 8; e++) v[e] = row[min(kg + e, k - 1)];
     }
 }
 
-__device__ __forceinline__ void stage_mask(float (&xv)[8], uint32_t k, const StageItem &it) {
+// Raw inputs of one item: x, plus up (kXSwiGLU) or the norm weight
+// (kXRmsNorm).  vec requires every input row to be 16-byte aligned.
+template <uint32_t XM>
+struct StageIn {
+    float x[8];
+    float a[8];
+};
+
+template <uint32_t XM>
+__device__ __forceinline__ void stage_load(StageIn<XM> &in, const GemvParams &p, const StageItem &it, bool vec) {
+    load8(in.x, p.x + (size_t)it.t * p.ldx, it.kg, p.k, vec);
+    if constexpr (XM == kXSwiGLU) load8(in.a, p.x2 + (size_t)it.t * p.ldx, it.kg, p.k, vec);
+    if constexpr (XM == kXRmsNorm) load8(in.a, p.norm_w, it.kg, p.k, vec);
+}
+
+// The staged values: the transform of the raw inputs, columns >= k zeroed.
+template <uint32_t XM>
+__device__ __forceinline__ void stage_finish(float (&xv)[8], const StageIn<XM> &in, uint32_t k, const StageItem &it,
+                                             const float *s_inv) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) xv[e] = (it.kg + e < k) ? xv[e] : 0.0f;
+    for (int e = 0; e < 8; e++) {
+        float v = in.x[e];
+        if constexpr (XM == kXSwiGLU) v = swiglu1(in.x[e], in.a[e]);
+        if constexpr (XM == kXRmsNorm) v = rmsnorm1(in.x[e], s_inv[it.t], in.a[e]);
+        xv[e] = (it.kg + e < k) ? v : 0.0f;
+    }
 }
 
 __device__ __forceinline__ void stage_store(uint8_t *lds, uint32_t m, const StageItem &it, const float (&xv)[8]) {
@@ -116,11 +146,90 @@ __device__ __forceinline__ uint32_t range_of(uint64_t block, uint32_t T, uint32_
     return (uint32_t)(((block + 1) * P + T - 1) / T) - 1;
 }
 
+// ---- RMSNorm prologue (kXRmsNorm) ----
+// The m rows of x are loaded once, kNormBatch float4s per thread (float4
+// slot v = token * slots + column/4; the host uses this mode only when
+// m * k fits), before the weight prologue.  Their squares go to LDS
+// lane-major, lane row (t*8 + j) holding columns j, j+8, ... of token t,
+// row stride norm_cols/8 + 4 floats.  Lane 8t + j of wavefront 0 then adds
+// its row in order; lanes are folded 0..7 per token.
+
+struct NormBatch {
+    float4 v[kGemvNormBatch];
+};
+
+// Loads are unconditional (addresses clamped into the row) and the values
+// are used only by norm_store, which masks columns past the row's end: a
+// load under a branch, or a use right after the loads, would make the
+// compiler wait for them before the weight prologue is issued.
+__device__ __forceinline__ void norm_load(NormBatch &nb, const GemvParams &p, uint32_t slots) {
+    const uint32_t n4 = p.m * slots, k = p.k;
+#pragma unroll
+    for (uint32_t u = 0; u < kGemvNormBatch; u++) {
+        const uint32_t v = min(u * kGemvThreads + threadIdx.x, n4 - 1);
+        const uint32_t t = v / slots, q = v - t * slots;
+        const float *row = p.x + (size_t)t * p.ldx;
+        if (p.x_vec) {   // k % 8 == 0: a slot is wholly inside or wholly past the row
+            nb.v[u] = *reinterpret_cast<const float4 *>(row + min(4 * q, k - 4));
+        } else {
+            nb.v[u].x = row[min(4 * q + 0, k - 1)];
+            nb.v[u].y = row[min(4 * q + 1, k - 1)];
+            nb.v[u].z = row[min(4 * q + 2, k - 1)];
+            nb.v[u].w = row[min(4 * q + 3, k - 1)];
+        }
+    }
+}
+
+__device__ __forceinline__ void norm_store(const NormBatch &nb, float *sq, uint32_t stride, uint32_t slots,
+                                           uint32_t k, uint32_t n4) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (uint32_t u = 0; u < kGemvNormBatch; u++) {
+        const uint32_t v = u * kGemvThreads + threadIdx.x;
+        // every loaded value is consumed here, repeats of a clamped slot too,
+        // so no load stays in flight past this point
+        const float4 x = nb.v[u];
+        const uint32_t t = min(v, n4 - 1) / slots, q = min(v, n4 - 1) - t * slots;
+        const uint32_t c = 4 * q;   // columns c .. c+3; past k they square to +0.0f
+        const float e0 = c + 0 < k ? x.x : 0.0f, e1 = c + 1 < k ? x.y : 0.0f;
+        const float e2 = c + 2 < k ? x.z : 0.0f, e3 = c + 3 < k ? x.w : 0.0f;
+        const float q0 = e0 * e0, q1 = e1 * e1, q2 = e2 * e2, q3 = e3 * e3;
+        if (v < n4) {
+            // lanes (c & 7) + 0..3 of token t, position q / 2
+            float *d = sq + (t * 8 + (c & 7)) * stride + (q >> 1);
+            d[0 * stride] = q0;
+            d[1 * stride] = q1;
+            d[2 * stride] = q2;
+            d[3 * stride] = q3;
+        }
+    }
+}
+
+// Lane 8t + j of wavefront 0 adds lane row 8t + j of the squares in order;
+// s_inv[t] = 1 / sqrtf(mean_t + eps) for t < m.
+__device__ __forceinline__ void norm_finish(const GemvParams &p, const float *sq, uint32_t stride, uint32_t cnt,
+                                            float *s_lane, float *s_inv) {
+#pragma clang fp contract(off)
+    const uint32_t tid = threadIdx.x;
+    if (tid < 8 * p.m) s_lane[tid] = lane_sum_in_order(sq + tid * stride, cnt, 0.0f);
+    __syncthreads();
+    if (tid < p.m) {
+        float s = s_lane[8 * tid];
+#pragma unroll
+        for (int j = 1; j < 8; j++) s = s + s_lane[8 * tid + j];
+        s_inv[tid] = rms_inverse(s, p.k, p.eps);
+    }
+    __syncthreads();
+}
+
 }  // namespace
 
+template <uint32_t XM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t s_ticket;
+    __shared__ float s_lane[8 * kGemvMaxM];   // kXRmsNorm: lane sums
+    __shared__ float s_inv[kGemvMaxM];        // kXRmsNorm: 1/rms per token
 
     // ---- segment and block range of this workgroup ----
     uint32_t si = 0;
@@ -169,28 +278,54 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     // ---- prologue: activation loads, then the first weight blocks ----
     const uint32_t per_t = nblk * 16;
     const uint32_t nvec = M * per_t;
-    float xpre[kStagePre][8];
+    const bool vec = p.x_vec != 0;
+    StageIn<XM> xpre[kStagePre];
+    auto stage_pre_load = [&]() {
 #pragma unroll
-    for (uint32_t u = 0; u < kStagePre; u++)   // index clamped: loads are unconditional
-        stage_load(xpre[u], p.x, p.ldx, p.k, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0),
-                   p.x_vec != 0);
-    __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t u = 0; u < kStagePre; u++)   // index clamped: loads are unconditional
+            stage_load(xpre[u], p, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0), vec);
+    };
+    auto ring_prologue = [&]() {
 #pragma unroll
-    for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], scs[d], min(b0 + d, b1 - 1));
-    __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], scs[d], min(b0 + d, b1 - 1));
+    };
+    if constexpr (XM == kXRmsNorm) {
+        // x rows first, alone: their squares go to LDS (the stage takes it
+        // over afterwards) before any weight load competes with them.  Then
+        // the stage and weight loads, whose latency hides behind the
+        // sequential sums.
+        const uint32_t slots = ((p.k + 7) & ~7u) / 4, stride = p.norm_cols / 8 + 4;
+        float *sq = reinterpret_cast<float *>(lds);
+        NormBatch nb;
+        norm_load(nb, p, slots);
+        norm_store(nb, sq, stride, slots, p.k, M * slots);
+        __syncthreads();
+        stage_pre_load();
+        __builtin_amdgcn_sched_barrier(0);
+        ring_prologue();
+        __builtin_amdgcn_sched_barrier(0);
+        norm_finish(p, sq, stride, slots / 2, s_lane, s_inv);
+    } else {
+        stage_pre_load();
+        __builtin_amdgcn_sched_barrier(0);
+        ring_prologue();
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // Split and stage while the weight blocks are in flight.
 #pragma unroll
     for (uint32_t u = 0; u < kStagePre; u++) {
         const uint32_t i = threadIdx.x + u * kGemvThreads;
         const StageItem it = stage_item(min(i, nvec - 1), per_t, KB, b0);
-        stage_mask(xpre[u], p.k, it);
-        if (i < nvec) stage_store(lds, M, it, xpre[u]);
+        float xv[8];
+        stage_finish(xv, xpre[u], p.k, it, s_inv);
+        if (i < nvec) stage_store(lds, M, it, xv);
     }
     for (uint32_t i = threadIdx.x + kStagePre * kGemvThreads; i < nvec; i += kGemvThreads) {
         const StageItem it = stage_item(i, per_t, KB, b0);
+        StageIn<XM> in;
+        stage_load(in, p, it, vec);
         float xv[8];
-        stage_load(xv, p.x, p.ldx, p.k, it, p.x_vec != 0);
-        stage_mask(xv, p.k, it);
+        stage_finish(xv, in, p.k, it, s_inv);
         stage_store(lds, M, it, xv);
     }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + zero_off)[threadIdx.x] = 0u;
@@ -239,7 +374,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t t = 4 * hh + r;
-                if (t < M && row < sg.rows) sg.y[(size_t)t * sg.ldy + row] = yv[r];
+                if (t < M && row < sg.rows) {
+                    const size_t o = (size_t)t * sg.ldy + row;
+                    sg.y[o] = sg.resid ? sg.resid[o] + yv[r] : yv[r];
+                }
             }
             return;
         }
@@ -333,7 +471,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
         for (uint32_t o = 0; o < kOut; o++) {
             const uint32_t i = threadIdx.x + o * kGemvThreads;
             const uint32_t t = i >> 7, r2 = G * kBlock + (i & 127);
-            if (i < per_c && r2 < sg.rows) sg.y[(size_t)t * sg.ldy + r2] = sum[o];
+            if (i < per_c && r2 < sg.rows) {
+                const size_t o2 = (size_t)t * sg.ldy + r2;
+                sg.y[o2] = sg.resid ? sg.resid[o2] + sum[o] : sum[o];
+            }
         }
         if (threadIdx.x == 0)
             __hip_atomic_store(p.cnt + sg.cnt_off + G, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -363,17 +504,37 @@ size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks) {
     return (size_t)range_blocks * kBlock * 3 * m * 2 + 16;   // + zero slot
 }
 
+bool gemv_norm_fits(uint32_t m, uint32_t k) {
+    return m >= 1 && m <= kGemvMaxM && (uint64_t)m * ((k + 7) & ~7u) <= kGemvThreads * kGemvNormBatch * 4;
+}
+
+uint32_t gemv_norm_cols(uint32_t k) { return (k + 31) & ~31u; }
+
+size_t gemv_norm_lds_bytes(uint32_t m, uint32_t norm_cols) {
+    return (size_t)m * 8 * (norm_cols / 8 + 4) * sizeof(float);
+}
+
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream) {
+    using Kernel = void (*)(GemvParams);
+    static const Kernel kernels[3] = {gemv_fp8_kernel<kXPlain>, gemv_fp8_kernel<kXRmsNorm>,
+                                      gemv_fp8_kernel<kXSwiGLU>};
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_fp8_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvMaxLds);
-        if (e != hipSuccess) return e;
+        for (Kernel k : kernels) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvMaxLds);
+            if (e != hipSuccess) return e;
+        }
         attr_set = true;
     }
-    const size_t lds = gemv_lds_bytes(p.m, p.max_range);
+    if (p.xmode > kXSwiGLU || p.m == 0 || p.m > kGemvMaxM) return hipErrorInvalidValue;
+    size_t lds = gemv_lds_bytes(p.m, p.max_range);
+    if (p.xmode == kXRmsNorm) {
+        if (!gemv_norm_fits(p.m, p.k) || p.norm_cols != gemv_norm_cols(p.k)) return hipErrorInvalidValue;
+        lds = std::max(lds, gemv_norm_lds_bytes(p.m, p.norm_cols));
+    }
     if (lds > kGemvMaxLds) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemv_fp8_kernel, dim3(p.nctas), dim3(kGemvThreads), lds, stream, p);
+    hipLaunchKernelGGL(kernels[p.xmode], dim3(p.nctas), dim3(kGemvThreads), lds, stream, p);
     return hipGetLastError();
 }
 

@@ -111,4 +111,73 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// ---- MLP neighbours, one element (qwen35-c/src/q35_kern.c) ----------------
+// Each operation rounds on its own (no contraction), as the reference's
+// q35_kern.c is compiled; division and square root are correctly rounded.
+
+// exp evaluated in double precision and rounded once to float.
+__device__ __forceinline__ float exp_rounded_once(float v) { return (float)exp((double)v); }
+
+// silu(g) * u as (g * (1 / (1 + exp(-g)))) * u  (q35_kern.c:70-73, :137-145).
+__device__ __forceinline__ float swiglu1(float g, float u) {
+#pragma clang fp contract(off)
+    const float sig = 1.0f / (1.0f + exp_rounded_once(-g));
+    const float t = g * sig;
+    return t * u;
+}
+
+// (x * inv) * (1 + w)  (q35_kern.c:77-86).
+__device__ __forceinline__ float rmsnorm1(float x, float inv, float w) {
+#pragma clang fp contract(off)
+    const float t = x * inv;
+    return t * (1.0f + w);
+}
+
+// 1 / sqrtf(s / n + eps) from a lane-folded sum of squares (q35_kern.c:80-81).
+__device__ __forceinline__ float rms_inverse(float s, uint32_t n, float eps) {
+#pragma clang fp contract(off)
+    const float mean = s / (float)n;
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// acc + s[0] + s[1] + ... + s[cnt-1], added one at a time in that order
+// (one lane of the reference's sum of squares).  s is 16-byte aligned LDS.
+// Blocks of 32 values alternate between two register sets, the reads of the
+// next block issued before the adds of the current one.
+__device__ __forceinline__ void add32_in_order(float &acc, const float4 (&v)[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        acc = acc + v[k].x;
+        acc = acc + v[k].y;
+        acc = acc + v[k].z;
+        acc = acc + v[k].w;
+    }
+}
+
+__device__ __forceinline__ void read32(float4 (&v)[8], const float4 *s4, uint32_t blk) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = s4[blk * 8 + k];
+}
+
+__device__ __forceinline__ float lane_sum_in_order(const float *s, uint32_t cnt, float acc) {
+#pragma clang fp contract(off)
+    const float4 *s4 = reinterpret_cast<const float4 *>(s);
+    const uint32_t n32 = cnt / 32;
+    float4 a[8], b[8];
+    if (n32) read32(a, s4, 0);
+    uint32_t blk = 0;
+    for (; blk + 2 <= n32; blk += 2) {
+        read32(b, s4, blk + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        add32_in_order(acc, a);
+        read32(a, s4, min(blk + 2, n32 - 1));   // the last pass re-reads a block: unused
+        __builtin_amdgcn_sched_barrier(0);
+        add32_in_order(acc, b);
+    }
+    if (blk < n32) add32_in_order(acc, a);
+    for (uint32_t t = n32 * 32; t < cnt; t++) acc = acc + s[t];
+    return acc;
+}
+
 }  // namespace q35mm

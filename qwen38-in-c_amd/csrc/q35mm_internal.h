@@ -43,6 +43,7 @@ struct GemvSeg {
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
+    const float *resid;  // optional [m][ldy]: y = resid + product (may equal y)
     uint32_t rows;
     uint32_t ldy;
     uint32_t nb;         // 128-row groups
@@ -53,9 +54,21 @@ struct GemvSeg {
     uint32_t cnt_off;    // offset of the segment's arrival counters [nb]
 };
 
+// What the staged activations are, per column k of token t:
+//   kXPlain    x[t][k]
+//   kXRmsNorm  (x[t][k] * inv_t) * (1 + norm_w[k]), inv_t the RMSNorm scale of
+//              row t of x, computed by every workgroup (q35_kern_rmsnorm)
+//   kXSwiGLU   silu(x[t][k]) * x2[t][k]  (q35_kern_swiglu; x = gate, x2 = up)
+constexpr uint32_t kXPlain = 0, kXRmsNorm = 1, kXSwiGLU = 2;
+
 struct GemvParams {
     GemvSeg seg[4];
     const float *x;      // [m][ldx] fp32
+    const float *x2;     // kXSwiGLU: up [m][ldx]
+    const float *norm_w; // kXRmsNorm: [k]
+    float eps;           // kXRmsNorm
+    uint32_t xmode;
+    uint32_t norm_cols;  // kXRmsNorm: k rounded up to 32
     float *ws;           // partial outputs
     uint32_t *cnt;       // arrival counters, zero between launches
     uint32_t ldx;
@@ -75,6 +88,13 @@ uint32_t gemv_ctas(uint32_t nblocks, uint32_t cus, uint32_t per_cu);
 // Most workgroups (P ranges) that can cover one group of kb blocks.
 uint32_t gemv_max_contrib(uint32_t nblocks, uint32_t nctas, uint32_t kb);
 size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks);
+// kXRmsNorm holds the m rows of x in registers, kGemvNormBatch float4s per
+// thread: usable when m * k (k rounded up to 8) fits.  norm_cols = k rounded
+// up to 32 sets the LDS layout of the squares.
+constexpr uint32_t kGemvNormBatch = 8;
+bool gemv_norm_fits(uint32_t m, uint32_t k);
+uint32_t gemv_norm_cols(uint32_t k);
+size_t gemv_norm_lds_bytes(uint32_t m, uint32_t norm_cols);
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
@@ -130,5 +150,13 @@ hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream
 // ---- BF16 matvec (q35_mm_bf16) ---------------------------------------
 hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols,
                             const float *x, float *y, hipStream_t stream);
+
+// ---- MLP neighbours (mlp.hip) -----------------------------------------
+// RMSNorm of rows rows of n (row strides ldx, ldy; y may alias x), SwiGLU
+// y = silu(g) * u, residual x += y.
+hipError_t launch_rmsnorm(const float *x, uint32_t ldx, const float *w, float *y, uint32_t ldy,
+                          uint32_t rows, uint32_t n, float eps, hipStream_t stream);
+hipError_t launch_swiglu(const float *g, const float *u, float *y, size_t n, hipStream_t stream);
+hipError_t launch_add_inplace(float *x, const float *y, size_t n, hipStream_t stream);
 
 }  // namespace q35mm

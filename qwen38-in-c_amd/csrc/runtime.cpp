@@ -76,12 +76,14 @@ struct Device {
     DevBuf cnt;       // arrival counters (uint32, zero between launches)
     DevBuf xb;        // bf16 lane-order activations for the GEMM
     DevBuf dx, dy;    // activation staging for the host-pointer ABI
+    DevBuf mlp;       // MLP block intermediates (xn, gate, up, y)
     void *pin = nullptr;   // pinned host staging
     size_t pin_cap = 0;
     uint32_t gemm_min_m = 64;
     uint32_t cus = 256;
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
+    bool mlp_unfused = false;   // Q35MM_MLP_UNFUSED=1: separate neighbour kernels on the GEMV path
 };
 
 std::recursive_mutex g_mu;
@@ -104,6 +106,7 @@ int ensure_device() {
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
+    g_dev.mlp_unfused = env_u32("Q35MM_MLP_UNFUSED", 0) != 0;
     g_dev.cus = (uint32_t)prop.multiProcessorCount;
     g_dev.gemv_per_cu = std::max(1u, env_u32("Q35MM_GEMV_CTAS_PER_CU", kGemvCtasPerCu));
     return Q35MM_OK;
@@ -212,17 +215,39 @@ std::vector<float> widen_scales(const uint16_t *sc, uint32_t rows, uint32_t cols
 // ---------------------------------------------------------------------
 // Dispatch
 // ---------------------------------------------------------------------
+// What the GEMV stages as activations (kXPlain: X itself; kXRmsNorm: the
+// RMSNorm of X with norm_w; kXSwiGLU: silu(X) * x2).
+struct GemvInput {
+    uint32_t xmode = kXPlain;
+    const float *x2 = nullptr;
+    const float *norm_w = nullptr;
+    float eps = 0.0f;
+};
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// SwiGLU costs every down-GEMV workgroup an exp per staged column and token;
+// beyond this many tokens the separate kernel (one exp per element) is
+// cheaper.
+constexpr uint32_t kMlpFusedSwiGLUMaxM = 2;
+
 int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
-                   float *const *dY, hipStream_t st) {
+                   float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid) {
     GemvParams p{};
     const uint32_t cols = w[0]->w.cols, KB = w[0]->w.kb;
     p.x = dX;
+    p.x2 = in.x2;
+    p.norm_w = in.norm_w;
+    p.eps = in.eps;
+    p.xmode = in.xmode;
+    p.norm_cols = in.xmode == kXRmsNorm ? gemv_norm_cols(cols) : 0;
     p.ldx = cols;
     p.m = m;
     p.k = cols;
     p.kb = KB;
     p.nseg = nseg;
-    p.x_vec = ((reinterpret_cast<uintptr_t>(dX) & 15) == 0 && cols % 8 == 0) ? 1u : 0u;
+    p.x_vec = (aligned16(dX) && cols % 8 == 0 && (!in.x2 || aligned16(in.x2)) &&
+               (!in.norm_w || aligned16(in.norm_w))) ? 1u : 0u;
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &ws = w[s]->w;
@@ -232,6 +257,7 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
         g.codes = ws.codes;
         g.scale = ws.scale;
         g.y = dY[s];
+        g.resid = resid ? resid[s] : nullptr;
         g.rows = ws.rows;
         g.ldy = ws.rows;
         g.nb = ws.nb;
@@ -258,13 +284,19 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
 }
 
 int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
-             float *const *dY, hipStream_t st) {
+             float *const *dY, hipStream_t st, const GemvInput &in = GemvInput(),
+             float *const *resid = nullptr) {
     const uint32_t cols = w[0]->w.cols;
     for (uint32_t t0 = 0; t0 < m; t0 += kGemvMaxM) {
         const uint32_t mg = std::min(kGemvMaxM, m - t0);
-        float *ys[4];
-        for (uint32_t s = 0; s < nseg; s++) ys[s] = dY[s] + (size_t)t0 * w[s]->w.rows;
-        int rc = run_gemv_group(w, nseg, mg, dX + (size_t)t0 * cols, ys, st);
+        float *ys[4], *rs[4];
+        for (uint32_t s = 0; s < nseg; s++) {
+            ys[s] = dY[s] + (size_t)t0 * w[s]->w.rows;
+            rs[s] = resid ? resid[s] + (size_t)t0 * w[s]->w.rows : nullptr;
+        }
+        GemvInput ig = in;
+        if (ig.x2) ig.x2 += (size_t)t0 * cols;
+        int rc = run_gemv_group(w, nseg, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr);
         if (rc) return rc;
     }
     return Q35MM_OK;
@@ -741,6 +773,99 @@ Q35MM_API int q35mm_bf16_gemv(const uint16_t *dW, uint32_t rows, uint32_t cols, 
     return Q35MM_OK;
 }
 
+Q35MM_API int q35mm_rmsnorm(const float *dX, const float *dW, float *dY, uint32_t rows, uint32_t n, float eps,
+                            void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (rows == 0 || n == 0) return Q35MM_OK;
+    if (!dX || !dW || !dY) return set_error(Q35MM_EINVAL, "null pointer");
+    HIP_TRY(launch_rmsnorm(dX, n, dW, dY, n, rows, n, eps, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_swiglu(const float *dGate, const float *dUp, float *dY, size_t n, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (n == 0) return Q35MM_OK;
+    if (!dGate || !dUp || !dY) return set_error(Q35MM_EINVAL, "null pointer");
+    HIP_TRY(launch_swiglu(dGate, dUp, dY, n, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const q35mm_weight *down,
+                        const float *dNormW, float eps, uint32_t m, float *dX, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (!rc) rc = check_weight(gate);
+    if (!rc) rc = check_weight(up);
+    if (!rc) rc = check_weight(down);
+    if (rc) return rc;
+    const uint32_t H = gate->w.cols, I = gate->w.rows;
+    if (up->w.cols != H || up->w.rows != I || down->w.cols != I || down->w.rows != H)
+        return set_error(Q35MM_EINVAL, "MLP shapes disagree: gate %ux%u up %ux%u down %ux%u", gate->w.rows,
+                         gate->w.cols, up->w.rows, up->w.cols, down->w.rows, down->w.cols);
+    if (m == 0) return Q35MM_OK;
+    if (!dX || !dNormW) return set_error(Q35MM_EINVAL, "null pointer");
+    // workspace: xn [m][H], g [m][I], u [m][I], y [m][H]; SwiGLU writes g in place
+    const size_t nh = (size_t)m * H, ni = (size_t)m * I;
+    rc = grow(g_dev.mlp, (2 * nh + 2 * ni) * sizeof(float), false);
+    if (rc) return rc;
+    float *xn = (float *)g_dev.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
+    hipStream_t st = pick_stream(stream);
+    const bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(gate->w, m) &&
+                      gemm_fits(up->w, m) && gemm_fits(down->w, m);
+    if (!gemm) {
+        // Decode.  RMSNorm inside the gate+up GEMV when a group's rows fit
+        // its registers (each workgroup forms the sums of squares itself),
+        // SwiGLU in the down GEMV's staging for groups of up to
+        // kMlpFusedSwiGLUMaxM tokens (every workgroup evaluates it for its
+        // own K range), the residual add always in the down GEMV's epilogue.
+        // Q35MM_MLP_UNFUSED=1 runs the separate kernels instead.
+        const uint32_t mg = std::min(m, kGemvMaxM);
+        const bool fuse_norm = !g_dev.mlp_unfused && gemv_norm_fits(mg, H);
+        const bool fuse_swiglu = !g_dev.mlp_unfused && m <= kMlpFusedSwiGLUMaxM;
+        const q35mm_weight *gu[2] = {gate, up};
+        float *gy[2] = {g, u};
+        GemvInput norm;
+        if (fuse_norm) {
+            norm.xmode = kXRmsNorm;
+            norm.norm_w = dNormW;
+            norm.eps = eps;
+            rc = run_gemv(gu, 2, m, dX, gy, st, norm);
+        } else {
+            HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
+            rc = run_gemv(gu, 2, m, xn, gy, st);
+        }
+        if (rc) return rc;
+        GemvInput sw;
+        if (fuse_swiglu) {
+            sw.xmode = kXSwiGLU;
+            sw.x2 = u;
+        } else {
+            HIP_TRY(launch_swiglu(g, u, g, ni, st));
+        }
+        const q35mm_weight *dn[1] = {down};
+        float *dy[1] = {dX};
+        if (!g_dev.mlp_unfused) return run_gemv(dn, 1, m, g, dy, st, sw, dy);
+        rc = run_gemv(dn, 1, m, g, &y, st, sw);
+        if (rc) return rc;
+        HIP_TRY(launch_add_inplace(dX, y, nh, st));
+        return Q35MM_OK;
+    }
+    HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
+    const q35mm_weight *gu[2] = {gate, up};
+    float *gy[2] = {g, u};
+    rc = q35mm_matmul_multi(gu, 2, m, xn, gy, stream);
+    if (rc) return rc;
+    HIP_TRY(launch_swiglu(g, u, g, ni, st));
+    rc = run_matmul(down, m, g, y, st);
+    if (rc) return rc;
+    HIP_TRY(launch_add_inplace(dX, y, nh, st));
+    return Q35MM_OK;
+}
+
 Q35MM_API void q35mm_release(const void *W) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     auto it = g_res.find(W);
@@ -765,7 +890,7 @@ Q35MM_API void q35mm_shutdown(void) {
     q35mm_release_all();
     if (g_dev.id < 0) return;
     (void)hipDeviceSynchronize();
-    for (DevBuf *b : {&g_dev.ws, &g_dev.cnt, &g_dev.xb, &g_dev.dx, &g_dev.dy}) {
+    for (DevBuf *b : {&g_dev.ws, &g_dev.cnt, &g_dev.xb, &g_dev.dx, &g_dev.dy, &g_dev.mlp}) {
         if (b->ptr) (void)hipFree(b->ptr);
         b->ptr = nullptr;
         b->cap = 0;

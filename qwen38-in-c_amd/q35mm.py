@@ -80,6 +80,9 @@ def _load(path: str = LIB_PATH) -> C.CDLL:
     lib.q35mm_dequant_f32.argtypes = [vp, vp, vp]
     lib.q35mm_decode_bf16.argtypes = [vp, vp, vp]
     lib.q35mm_bf16_gemv.argtypes = [vp, C.c_uint32, C.c_uint32, vp, vp, vp]
+    lib.q35mm_rmsnorm.argtypes = [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_float, vp]
+    lib.q35mm_swiglu.argtypes = [vp, vp, vp, C.c_size_t, vp]
+    lib.q35mm_mlp.argtypes = [vp, vp, vp, vp, C.c_float, C.c_uint32, vp, vp]
     lib.q35mm_release.argtypes = [vp]
     lib.q35mm_release.restype = None
     lib.q35mm_release_all.argtypes = []
@@ -305,6 +308,30 @@ def bf16_gemv(W16, x, y, stream=None) -> None:
     rows, cols = W16.shape
     _check(lib.q35mm_bf16_gemv(_dptr(W16), rows, cols, _dptr(x), _dptr(y), _stream(stream)),
            "q35mm_bf16_gemv")
+
+
+def rmsnorm(X, w, Y, eps: float = 1e-6, stream=None) -> None:
+    """Row-wise zero-centred RMSNorm (q35_kern_rmsnorm) of X [rows][n]."""
+    n = X.shape[-1]
+    rows = X.numel() // n if n else 0
+    if w.numel() != n or Y.numel() != X.numel():
+        raise Q35mmError("rmsnorm: shapes disagree")
+    _check(lib.q35mm_rmsnorm(_dptr(X), _dptr(w), _dptr(Y), rows, n, eps, _stream(stream)), "q35mm_rmsnorm")
+
+
+def swiglu(G, U, Y, stream=None) -> None:
+    """Y = silu(G) * U elementwise (q35_kern_swiglu)."""
+    if G.numel() != U.numel() or Y.numel() != G.numel():
+        raise Q35mmError("swiglu: sizes disagree")
+    _check(lib.q35mm_swiglu(_dptr(G), _dptr(U), _dptr(Y), G.numel(), _stream(stream)), "q35mm_swiglu")
+
+
+def mlp(gate: Weight, up: Weight, down: Weight, norm_w, X, eps: float = 1e-6, m: int | None = None,
+        stream=None) -> None:
+    """One MLP block in place on the residual stream X [m][H]."""
+    m = X.shape[0] if m is None else m
+    _check(lib.q35mm_mlp(gate.handle, up.handle, down.handle, _dptr(norm_w), eps, m, _dptr(X),
+                         _stream(stream)), "q35mm_mlp")
 
 
 def shutdown() -> None:

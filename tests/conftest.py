@@ -43,6 +43,15 @@ def ref():
 
 
 @pytest.fixture(scope="session")
+def refkern():
+    """The reference's own compiled q35_kern.c (oracle/_ref), when built."""
+    from oracle import RefKern
+    if not RefKern.available():
+        pytest.skip("oracle/_ref not built (reference tree absent when built)")
+    return RefKern()
+
+
+@pytest.fixture(scope="session")
 def q():
     import q35mm
     return q35mm
@@ -81,6 +90,27 @@ def load_fixture(name: str):
 def fixture_names(fp8=True):
     man = json.load(open(os.path.join(GOLDEN, "mm", "manifest.json")))
     return [c["name"] for c in man if c["fp8"] == fp8]
+
+
+def kern_manifest():
+    return json.load(open(os.path.join(GOLDEN, "kern", "manifest.json")))
+
+
+def load_kern_fixture(name: str):
+    """(case, inputs, expected) of a reference kernel fixture copied to
+    tests/golden/kern (qwen35-c/tests/fixtures/kern)."""
+    c = kern_manifest()[name]
+    d = os.path.join(GOLDEN, "kern")
+    ins = [np.fromfile(os.path.join(d, f), np.float32) for f in c["in"]]
+    return c, ins, np.fromfile(os.path.join(d, c["out"]), np.float32)
+
+
+def within_kern_tol(y, yref, atol, rtol) -> bool:
+    """The reference kernel test's acceptance rule
+    (qwen35-c/tests/test_kern.c:112-121): |y - ref| <= atol + rtol*|ref|."""
+    y = np.asarray(y, np.float64)
+    yref = np.asarray(yref, np.float64)
+    return bool((np.abs(y - yref) <= atol + rtol * np.abs(yref)).all())
 
 
 def goldens():
