@@ -36,7 +36,11 @@ enum {
     Q35MM_EINVAL = -1,    /* bad argument (null pointer, size out of range) */
     Q35MM_EHIP = -2,      /* a HIP runtime call failed */
     Q35MM_ENOMEM = -3,    /* device or host allocation failed */
-    Q35MM_ENODEV = -4     /* no usable gfx950 device */
+    Q35MM_ENODEV = -4,    /* no usable gfx950 device */
+    Q35MM_EIO = -5,       /* a checkpoint file cannot be opened or read */
+    Q35MM_EFORMAT = -6,   /* bad safetensors header, unknown dtype, range out of file */
+    Q35MM_ENOTFOUND = -7, /* no tensor of that name */
+    Q35MM_ESHAPE = -8     /* tensor dtype / rank / shape differs from what was asked */
 };
 
 typedef struct q35mm_weight q35mm_weight;
@@ -115,6 +119,49 @@ int q35mm_swiglu(const float *dGate, const float *dUp, float *dY, size_t n,
 int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up,
               const q35mm_weight *down, const float *dNormW, float eps,
               uint32_t m, float *dX, void *stream);
+
+/* ---- checkpoint -> HBM (safetensors) ---------------------------------- */
+
+/* The loader-side quantizer of qwen35-c/src/q35_model.c:302-350 (bind_ab) on
+ * device pointers: dW [rows][cols] fp32 -> dCodes [rows][cols] row-major e4m3
+ * and dScale [ceil(rows/128)][ceil(cols/128)] bf16 bits.  Per 128x128 block:
+ * scale = bf16(amax / 448); codes = nearest e4m3 of w / scale (ties to the
+ * even code, saturating at 448, NaN -> 0x7F); blocks with scale 0 keep zero
+ * codes.  Code-for-code equal to the reference. */
+int q35mm_quantize_f32(const float *dW, uint32_t rows, uint32_t cols,
+                       uint8_t *dCodes, uint16_t *dScale, void *stream);
+
+/* A safetensors checkpoint: one .safetensors file, or a directory whose
+ * files with ".safetensors" in the name (and not "json") are its shards
+ * (qwen35-c/include/q35/q35_st.h:44-53).  Opening parses and validates every
+ * header (Q35MM_EFORMAT / Q35MM_EIO on failure); tensor bytes are read on
+ * demand. */
+typedef struct q35mm_st q35mm_st;
+int q35mm_st_open(const char *path, q35mm_st **out);
+void q35mm_st_close(q35mm_st *st);
+uint32_t q35mm_st_count(const q35mm_st *st);
+const char *q35mm_st_name(const q35mm_st *st, uint32_t i);
+/* dtype is one of "F8_E4M3", "BF16", "F32", "F16", "I64". */
+int q35mm_st_info(const q35mm_st *st, const char *name, const char **dtype,
+                  uint32_t *ndim, uint32_t shape[8], uint64_t *nbytes);
+/* The tensor's bytes into host memory dst (cap >= its size). */
+int q35mm_st_read(const q35mm_st *st, const char *name, void *dst, uint64_t cap);
+/* bind_fp8 (qwen35-c/src/q35_model.c:253-273): F8_E4M3 `name` [rows][cols]
+ * and BF16 `name`_scale_inv [ceil(rows/128)][ceil(cols/128)] -> a resident
+ * weight, read in chunks into pinned memory, copied to HBM and repacked on
+ * the device.  Q35MM_ENOTFOUND / Q35MM_ESHAPE as the reference's checks. */
+int q35mm_st_load_fp8(q35mm_st *st, const char *name, uint32_t rows,
+                      uint32_t cols, q35mm_weight **out);
+/* bind_ab (qwen35-c/src/q35_model.c:302-350): as q35mm_st_load_fp8 when the
+ * tensor is F8_E4M3; a BF16 [rows][cols] tensor is quantized on the device
+ * (as q35mm_quantize_f32). */
+int q35mm_st_load_ab(q35mm_st *st, const char *name, uint32_t rows,
+                     uint32_t cols, q35mm_weight **out);
+/* A BF16 [rows][cols] tensor (the lm_head of q35_mm_bf16) into a new device
+ * buffer *dOut, released with q35mm_free. */
+int q35mm_st_load_bf16(q35mm_st *st, const char *name, uint32_t rows,
+                       uint32_t cols, uint16_t **dOut);
+void q35mm_free(void *dptr);
 
 /* Drop the resident copy that the q35_mm_* entry points made for host
  * pointer W (no-op if none).  q35mm_release_all drops every such copy. */

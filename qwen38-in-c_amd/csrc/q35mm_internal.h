@@ -151,6 +151,15 @@ hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream
 hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols,
                             const float *x, float *y, hipStream_t stream);
 
+// ---- load-time quantizer (quantize.hip) --------------------------------
+// w [rows][cols] (fp32, or bf16 bits) -> row-major e4m3 codes and the
+// [ceil(rows/128)][ceil(cols/128)] block scales as bf16 bits and/or fp32
+// (either pointer may be null).
+hipError_t launch_quantize_f32(const float *w, uint32_t rows, uint32_t cols, uint8_t *codes, uint16_t *scale_bf16,
+                               float *scale_f32, hipStream_t stream);
+hipError_t launch_quantize_bf16(const uint16_t *w, uint32_t rows, uint32_t cols, uint8_t *codes,
+                                uint16_t *scale_bf16, float *scale_f32, hipStream_t stream);
+
 // ---- MLP neighbours (mlp.hip) -----------------------------------------
 // RMSNorm of rows rows of n (row strides ldx, ldy; y may alias x), SwiGLU
 // y = silu(g) * u, residual x += y.

@@ -11,12 +11,14 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "q35/q35_mm.h"
 #include "q35mm/q35mm.h"
 #include "q35mm_internal.h"
+#include "safetensors.h"
 
 #define Q35MM_API extern "C" __attribute__((visibility("default")))
 
@@ -25,6 +27,10 @@ using namespace q35mm;
 struct q35mm_weight {
     Weight w;
     size_t bytes = 0;
+};
+
+struct q35mm_st {
+    st::Archive a;
 };
 
 namespace {
@@ -77,6 +83,8 @@ struct Device {
     DevBuf xb;        // bf16 lane-order activations for the GEMM
     DevBuf dx, dy;    // activation staging for the host-pointer ABI
     DevBuf mlp;       // MLP block intermediates (xn, gate, up, y)
+    void *up_pin[4] = {};        // pinned chunks of the file -> HBM upload ring
+    hipEvent_t up_ev[4] = {};
     void *pin = nullptr;   // pinned host staging
     size_t pin_cap = 0;
     uint32_t gemm_min_m = 64;
@@ -152,9 +160,12 @@ int grow_pinned(size_t bytes) {
 // ---------------------------------------------------------------------
 // Weight upload
 // ---------------------------------------------------------------------
-int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t rows, uint32_t cols,
-                  q35mm_weight **out) {
-    if (!W || !scale_f32_rowmajor || !out) return set_error(Q35MM_EINVAL, "null argument");
+// Allocates a resident weight, lets fill() put the row-major e4m3 codes into
+// the device staging buffer raw and the fp32 block scales into w.scale
+// (asynchronously on st), then repacks raw into the lane-order tiles.
+template <typename Fill>
+int weight_build(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
+    if (!out) return set_error(Q35MM_EINVAL, "null argument");
     if (rows == 0 || cols == 0) return set_error(Q35MM_EINVAL, "empty weight %ux%u", rows, cols);
     int rc = ensure_device();
     if (rc) return rc;
@@ -169,6 +180,7 @@ int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t ro
     const size_t raw_bytes = (size_t)rows * cols;
     uint8_t *raw = nullptr;
     auto fail = [&](int code) {
+        (void)hipStreamSynchronize(g_dev.stream);
         if (raw) (void)hipFree(raw);
         if (h->w.codes) (void)hipFree(h->w.codes);
         if (h->w.scale) (void)hipFree(h->w.scale);
@@ -188,18 +200,26 @@ int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t ro
         return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for staging failed", raw_bytes));
     }
     hipStream_t st = g_dev.stream;
-    if (hipMemcpyAsync(raw, W, raw_bytes, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(h->w.scale, scale_f32_rowmajor, scale_bytes, hipMemcpyHostToDevice, st) !=
-            hipSuccess ||
-        launch_repack(raw, rows, cols, nb, kb, h->w.codes, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
-        return fail(set_error(Q35MM_EHIP, "weight upload failed: %s",
-                              hipGetErrorString(hipGetLastError())));
+    rc = fill(h->w, raw, st);
+    if (rc) return fail(rc);
+    if (launch_repack(raw, rows, cols, nb, kb, h->w.codes, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return fail(set_error(Q35MM_EHIP, "weight upload failed: %s", hipGetErrorString(hipGetLastError())));
     (void)hipFree(raw);
     raw = nullptr;
     h->bytes = tiled_bytes + scale_bytes;
     *out = h;
     return Q35MM_OK;
+}
+
+int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t rows, uint32_t cols,
+                  q35mm_weight **out) {
+    if (!W || !scale_f32_rowmajor) return set_error(Q35MM_EINVAL, "null argument");
+    return weight_build(rows, cols, out, [&](Weight &w, uint8_t *raw, hipStream_t st) -> int {
+        HIP_TRY(hipMemcpyAsync(raw, W, (size_t)rows * cols, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(w.scale, scale_f32_rowmajor, (size_t)w.nb * w.kb * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+        return Q35MM_OK;
+    });
 }
 
 std::vector<float> widen_scales(const uint16_t *sc, uint32_t rows, uint32_t cols) {
@@ -354,6 +374,131 @@ int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hi
     const q35mm_weight *ws[1] = {w};
     float *ys[1] = {dY};
     return run_gemv(ws, 1, m, dX, ys, st);
+}
+
+// ---------------------------------------------------------------------
+// Checkpoint (safetensors) -> HBM
+// ---------------------------------------------------------------------
+constexpr size_t kUpChunk = 16u << 20;   // bytes per pinned chunk
+constexpr int kUpBufs = 4;
+constexpr int kUpReaders = 4;            // threads reading one chunk from the file
+
+int upload_ring() {
+    for (int i = 0; i < kUpBufs; i++) {
+        if (g_dev.up_pin[i]) continue;
+        if (hipHostMalloc(&g_dev.up_pin[i], kUpChunk, hipHostMallocDefault) != hipSuccess) {
+            g_dev.up_pin[i] = nullptr;
+            return set_error(Q35MM_ENOMEM, "hipHostMalloc(%zu) for the upload ring failed", kUpChunk);
+        }
+        HIP_TRY(hipEventCreateWithFlags(&g_dev.up_ev[i], hipEventDisableTiming));
+    }
+    return Q35MM_OK;
+}
+
+// Tensor bytes [0, t.bytes) -> device dst, asynchronously on st: the file is
+// read in 16 MiB chunks (kUpReaders threads per chunk) into a ring of pinned
+// buffers, each copied to HBM while the next one is read.  Complete once st
+// is synchronised.
+int upload_tensor(const st::Archive &a, const st::Tensor &t, void *dst, hipStream_t st) {
+    int rc = upload_ring();
+    if (rc) return rc;
+    for (int i = 0; i < kUpBufs; i++) HIP_TRY(hipEventSynchronize(g_dev.up_ev[i]));
+    uint8_t *d = static_cast<uint8_t *>(dst);
+    size_t i = 0;
+    for (uint64_t off = 0; off < t.bytes; off += kUpChunk, i++) {
+        const int b = (int)(i % kUpBufs);
+        if (i >= (size_t)kUpBufs) HIP_TRY(hipEventSynchronize(g_dev.up_ev[b]));
+        const uint64_t len = std::min<uint64_t>(kUpChunk, t.bytes - off);
+        uint8_t *pin = static_cast<uint8_t *>(g_dev.up_pin[b]);
+        bool ok = true;
+        if (len >= (4u << 20)) {
+            const uint64_t part = (len / kUpReaders + 4095) & ~(uint64_t)4095;
+            bool oks[kUpReaders];
+            std::thread th[kUpReaders - 1];
+            auto rd = [&](int k) {
+                const uint64_t o = std::min<uint64_t>(len, part * k), e = std::min<uint64_t>(len, o + part);
+                oks[k] = e <= o || a.read(t, off + o, e - o, pin + o);
+            };
+            for (int k = 1; k < kUpReaders; k++) th[k - 1] = std::thread(rd, k);
+            rd(0);
+            for (auto &x : th) x.join();
+            for (bool o : oks) ok = ok && o;
+        } else {
+            ok = a.read(t, off, len, pin);
+        }
+        if (!ok) return set_error(Q35MM_EIO, "read of %s (%llu bytes at %llu) failed", t.name.c_str(),
+                                  (unsigned long long)len, (unsigned long long)off);
+        HIP_TRY(hipMemcpyAsync(d + off, pin, len, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipEventRecord(g_dev.up_ev[b], st));
+    }
+    return Q35MM_OK;
+}
+
+// The reference loader's strict lookup (qwen35-c/src/q35_model.c:225-249):
+// present, of dtype dt, with exactly these dims.
+int need_tensor(const st::Archive &a, const char *name, int dt, uint32_t ndim, const uint32_t *shape,
+                const st::Tensor **out) {
+    const st::Tensor *t = a.find(name);
+    if (!t) return set_error(Q35MM_ENOTFOUND, "missing tensor: %s", name);
+    if (t->dtype != dt)
+        return set_error(Q35MM_ESHAPE, "tensor %s: dtype %s, want %s", name, st::dtype_name(t->dtype),
+                         st::dtype_name(dt));
+    if (t->ndim != ndim) return set_error(Q35MM_ESHAPE, "tensor %s: ndim %u, want %u", name, t->ndim, ndim);
+    for (uint32_t i = 0; i < ndim; i++)
+        if (t->shape[i] != shape[i])
+            return set_error(Q35MM_ESHAPE, "tensor %s: shape[%u]=%u, want %u", name, i, t->shape[i], shape[i]);
+    *out = t;
+    return Q35MM_OK;
+}
+
+// bind_fp8 (qwen35-c/src/q35_model.c:253-273): F8_E4M3 [rows][cols] plus
+// BF16 "<name>_scale_inv" [ceil(rows/128)][ceil(cols/128)], uploaded and
+// repacked on the device.
+int st_load_fp8(const st::Archive &a, const char *name, uint32_t rows, uint32_t cols, q35mm_weight **out) {
+    const uint32_t wshape[2] = {rows, cols}, sshape[2] = {(rows + 127) / 128, (cols + 127) / 128};
+    const st::Tensor *tw = nullptr, *ts = nullptr;
+    int rc = need_tensor(a, name, st::kF8E4M3, 2, wshape, &tw);
+    if (rc) return rc;
+    const std::string sname = std::string(name) + "_scale_inv";
+    rc = need_tensor(a, sname.c_str(), st::kBF16, 2, sshape, &ts);
+    if (rc) return rc;
+    std::vector<uint16_t> sc((size_t)sshape[0] * sshape[1]);
+    if (!a.read(*ts, 0, ts->bytes, sc.data())) return set_error(Q35MM_EIO, "read of %s failed", sname.c_str());
+    const std::vector<float> f = widen_scales(sc.data(), rows, cols);
+    return weight_build(rows, cols, out, [&](Weight &w, uint8_t *raw, hipStream_t st) -> int {
+        HIP_TRY(hipMemcpyAsync(w.scale, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice, st));
+        return upload_tensor(a, *tw, raw, st);
+    });
+}
+
+// bind_ab (qwen35-c/src/q35_model.c:302-350): an F8_E4M3 tensor binds as
+// above; a BF16 [rows][cols] tensor is uploaded and quantized on the device
+// (quantize.hip), codes going straight to the repack.
+int st_load_ab(const st::Archive &a, const char *name, uint32_t rows, uint32_t cols, q35mm_weight **out) {
+    const st::Tensor *t = a.find(name);
+    if (!t) return set_error(Q35MM_ENOTFOUND, "missing tensor: %s", name);
+    if (t->dtype == st::kF8E4M3) return st_load_fp8(a, name, rows, cols, out);
+    if (t->dtype != st::kBF16)
+        return set_error(Q35MM_ESHAPE, "tensor %s: dtype %s, want BF16 or F8_E4M3", name, st::dtype_name(t->dtype));
+    const uint32_t wshape[2] = {rows, cols};
+    int rc = need_tensor(a, name, st::kBF16, 2, wshape, &t);
+    if (rc) return rc;
+    uint16_t *src = nullptr;
+    rc = weight_build(rows, cols, out, [&](Weight &w, uint8_t *raw, hipStream_t st) -> int {
+        if (hipMalloc(&src, t->bytes) != hipSuccess) {
+            src = nullptr;
+            return set_error(Q35MM_ENOMEM, "hipMalloc(%llu) for bf16 staging failed", (unsigned long long)t->bytes);
+        }
+        int r = upload_tensor(a, *t, src, st);
+        if (r) return r;
+        HIP_TRY(launch_quantize_bf16(src, rows, cols, raw, nullptr, w.scale, st));
+        return Q35MM_OK;
+    });
+    if (src) {
+        (void)hipStreamSynchronize(g_dev.stream);
+        (void)hipFree(src);
+    }
+    return rc;
 }
 
 // ---------------------------------------------------------------------
@@ -866,6 +1011,105 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
     return Q35MM_OK;
 }
 
+Q35MM_API int q35mm_quantize_f32(const float *dW, uint32_t rows, uint32_t cols, uint8_t *dCodes,
+                                 uint16_t *dScale, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return Q35MM_OK;
+    if (!dW || !dCodes || !dScale) return set_error(Q35MM_EINVAL, "null pointer");
+    HIP_TRY(launch_quantize_f32(dW, rows, cols, dCodes, dScale, nullptr, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_st_open(const char *path, q35mm_st **out) {
+    if (!path || !out) return set_error(Q35MM_EINVAL, "null argument");
+    auto *h = new q35mm_st();
+    std::string msg;
+    const int s = h->a.open(path, msg);
+    if (s != st::kOk) {
+        delete h;
+        *out = nullptr;
+        return set_error(s == st::kOpen || s == st::kIo ? Q35MM_EIO : Q35MM_EFORMAT, "%s: %s",
+                         st::status_str(s), msg.c_str());
+    }
+    *out = h;
+    return Q35MM_OK;
+}
+
+Q35MM_API void q35mm_st_close(q35mm_st *st) { delete st; }
+
+Q35MM_API uint32_t q35mm_st_count(const q35mm_st *st) { return st ? (uint32_t)st->a.tensors.size() : 0u; }
+
+Q35MM_API const char *q35mm_st_name(const q35mm_st *st, uint32_t i) {
+    return st && i < st->a.tensors.size() ? st->a.tensors[i].name.c_str() : nullptr;
+}
+
+Q35MM_API int q35mm_st_info(const q35mm_st *st, const char *name, const char **dtype, uint32_t *ndim,
+                            uint32_t shape[8], uint64_t *nbytes) {
+    if (!st || !name) return set_error(Q35MM_EINVAL, "null argument");
+    const st::Tensor *t = st->a.find(name);
+    if (!t) return set_error(Q35MM_ENOTFOUND, "missing tensor: %s", name);
+    if (dtype) *dtype = st::dtype_name(t->dtype);
+    if (ndim) *ndim = t->ndim;
+    if (shape)
+        for (int i = 0; i < 8; i++) shape[i] = t->shape[i];
+    if (nbytes) *nbytes = t->bytes;
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_st_read(const q35mm_st *st, const char *name, void *dst, uint64_t cap) {
+    if (!st || !name || !dst) return set_error(Q35MM_EINVAL, "null argument");
+    const st::Tensor *t = st->a.find(name);
+    if (!t) return set_error(Q35MM_ENOTFOUND, "missing tensor: %s", name);
+    if (cap < t->bytes) return set_error(Q35MM_EINVAL, "buffer of %llu bytes for %s (%llu bytes)",
+                                         (unsigned long long)cap, name, (unsigned long long)t->bytes);
+    if (!st->a.read(*t, 0, t->bytes, dst)) return set_error(Q35MM_EIO, "read of %s failed", name);
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_st_load_fp8(q35mm_st *st, const char *name, uint32_t rows, uint32_t cols, q35mm_weight **out) {
+    if (!st || !name || !out) return set_error(Q35MM_EINVAL, "null argument");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return st_load_fp8(st->a, name, rows, cols, out);
+}
+
+Q35MM_API int q35mm_st_load_ab(q35mm_st *st, const char *name, uint32_t rows, uint32_t cols, q35mm_weight **out) {
+    if (!st || !name || !out) return set_error(Q35MM_EINVAL, "null argument");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return st_load_ab(st->a, name, rows, cols, out);
+}
+
+Q35MM_API int q35mm_st_load_bf16(q35mm_st *st, const char *name, uint32_t rows, uint32_t cols, uint16_t **dOut) {
+    if (!st || !name || !dOut) return set_error(Q35MM_EINVAL, "null argument");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    const uint32_t shape[2] = {rows, cols};
+    const st::Tensor *t = nullptr;
+    rc = need_tensor(st->a, name, st::kBF16, 2, shape, &t);
+    if (rc) return rc;
+    uint16_t *d = nullptr;
+    if (hipMalloc(&d, t->bytes) != hipSuccess)
+        return set_error(Q35MM_ENOMEM, "hipMalloc(%llu) failed", (unsigned long long)t->bytes);
+    rc = upload_tensor(st->a, *t, d, g_dev.stream);
+    if (!rc && hipStreamSynchronize(g_dev.stream) != hipSuccess) rc = set_error(Q35MM_EHIP, "upload failed");
+    if (rc) {
+        (void)hipStreamSynchronize(g_dev.stream);
+        (void)hipFree(d);
+        return rc;
+    }
+    *dOut = d;
+    return Q35MM_OK;
+}
+
+Q35MM_API void q35mm_free(void *dptr) {
+    if (!dptr) return;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(dptr);
+}
+
 Q35MM_API void q35mm_release(const void *W) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     auto it = g_res.find(W);
@@ -898,6 +1142,12 @@ Q35MM_API void q35mm_shutdown(void) {
     if (g_dev.pin) (void)hipHostFree(g_dev.pin);
     g_dev.pin = nullptr;
     g_dev.pin_cap = 0;
+    for (int i = 0; i < 4; i++) {
+        if (g_dev.up_pin[i]) (void)hipHostFree(g_dev.up_pin[i]);
+        if (g_dev.up_ev[i]) (void)hipEventDestroy(g_dev.up_ev[i]);
+        g_dev.up_pin[i] = nullptr;
+        g_dev.up_ev[i] = nullptr;
+    }
     if (g_dev.stream) (void)hipStreamDestroy(g_dev.stream);
     g_dev.stream = nullptr;
     g_dev.id = -1;

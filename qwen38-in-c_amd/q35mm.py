@@ -83,6 +83,21 @@ def _load(path: str = LIB_PATH) -> C.CDLL:
     lib.q35mm_rmsnorm.argtypes = [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_float, vp]
     lib.q35mm_swiglu.argtypes = [vp, vp, vp, C.c_size_t, vp]
     lib.q35mm_mlp.argtypes = [vp, vp, vp, vp, C.c_float, C.c_uint32, vp, vp]
+    lib.q35mm_quantize_f32.argtypes = [vp, C.c_uint32, C.c_uint32, vp, vp, vp]
+    lib.q35mm_st_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+    lib.q35mm_st_close.argtypes = [vp]
+    lib.q35mm_st_close.restype = None
+    lib.q35mm_st_count.argtypes = [vp]
+    lib.q35mm_st_count.restype = C.c_uint32
+    lib.q35mm_st_name.argtypes = [vp, C.c_uint32]
+    lib.q35mm_st_name.restype = C.c_char_p
+    lib.q35mm_st_info.argtypes = [vp, C.c_char_p, C.POINTER(C.c_char_p), _u32p, _u32p, C.POINTER(C.c_uint64)]
+    lib.q35mm_st_read.argtypes = [vp, C.c_char_p, vp, C.c_uint64]
+    for name in ("q35mm_st_load_fp8", "q35mm_st_load_ab"):
+        getattr(lib, name).argtypes = [vp, C.c_char_p, C.c_uint32, C.c_uint32, C.POINTER(vp)]
+    lib.q35mm_st_load_bf16.argtypes = [vp, C.c_char_p, C.c_uint32, C.c_uint32, C.POINTER(vp)]
+    lib.q35mm_free.argtypes = [vp]
+    lib.q35mm_free.restype = None
     lib.q35mm_release.argtypes = [vp]
     lib.q35mm_release.restype = None
     lib.q35mm_release_all.argtypes = []
@@ -105,7 +120,9 @@ def _p(a: np.ndarray, ptype):
 
 def _check(rc: int, what: str) -> None:
     if rc != 0:
-        raise Q35mmError(f"{what} failed ({rc}): {lib.q35mm_last_error().decode()}")
+        err = Q35mmError(f"{what} failed ({rc}): {lib.q35mm_last_error().decode()}")
+        err.code = rc
+        raise err
 
 
 # ---------------------------------------------------------------------------
@@ -332,6 +349,77 @@ def mlp(gate: Weight, up: Weight, down: Weight, norm_w, X, eps: float = 1e-6, m:
     m = X.shape[0] if m is None else m
     _check(lib.q35mm_mlp(gate.handle, up.handle, down.handle, _dptr(norm_w), eps, m, _dptr(X),
                          _stream(stream)), "q35mm_mlp")
+
+
+def quantize_f32(W, codes, scale, stream=None) -> None:
+    """Device quantizer (q35mm_quantize_f32): W [rows][cols] fp32 ->
+    codes [rows][cols] uint8, scale [ceil(rows/128)][ceil(cols/128)] bf16 bits."""
+    rows, cols = W.shape
+    _check(lib.q35mm_quantize_f32(_dptr(W), rows, cols, _dptr(codes), _dptr(scale), _stream(stream)),
+           "q35mm_quantize_f32")
+
+
+class Checkpoint:
+    """A safetensors file or shard directory (q35mm_st_open)."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        _check(lib.q35mm_st_open(os.fsencode(path), C.byref(h)), "q35mm_st_open")
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            lib.q35mm_st_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def names(self) -> list:
+        return [lib.q35mm_st_name(self.handle, i).decode() for i in range(lib.q35mm_st_count(self.handle))]
+
+    def info(self, name: str):
+        """(dtype, shape, nbytes)"""
+        dt = C.c_char_p()
+        nd = C.c_uint32()
+        shape = (C.c_uint32 * 8)()
+        nb = C.c_uint64()
+        _check(lib.q35mm_st_info(self.handle, name.encode(), C.byref(dt), C.byref(nd), shape, C.byref(nb)),
+               "q35mm_st_info")
+        return dt.value.decode(), tuple(shape[: nd.value]), nb.value
+
+    def read(self, name: str) -> bytes:
+        _, _, nb = self.info(name)
+        buf = C.create_string_buffer(max(nb, 1))
+        _check(lib.q35mm_st_read(self.handle, name.encode(), buf, nb), "q35mm_st_read")
+        return buf.raw[:nb]
+
+    def _load(self, fn, name, rows, cols) -> "Weight":
+        w = Weight.__new__(Weight)
+        w.rows, w.cols = rows, cols
+        h = C.c_void_p()
+        _check(getattr(lib, fn)(self.handle, name.encode(), rows, cols, C.byref(h)), fn)
+        w.handle = h
+        return w
+
+    def load_fp8(self, name: str, rows: int, cols: int) -> "Weight":
+        return self._load("q35mm_st_load_fp8", name, rows, cols)
+
+    def load_ab(self, name: str, rows: int, cols: int) -> "Weight":
+        return self._load("q35mm_st_load_ab", name, rows, cols)
+
+    def load_bf16(self, name: str, rows: int, cols: int) -> int:
+        """Device pointer of a new bf16 buffer (free with free())."""
+        p = C.c_void_p()
+        _check(lib.q35mm_st_load_bf16(self.handle, name.encode(), rows, cols, C.byref(p)), "q35mm_st_load_bf16")
+        return p.value
+
+
+def free(dptr: int) -> None:
+    lib.q35mm_free(dptr)
 
 
 def shutdown() -> None:
