@@ -84,6 +84,7 @@ struct Device {
     DevBuf dx, dy;    // activation staging for the host-pointer ABI
     DevBuf mlp;       // MLP block intermediates (xn, gate, up, y)
     void *up_pin[4] = {};        // pinned chunks of the file -> HBM upload ring
+    void *up_dev[4] = {};        // device side of each chunk (+ room for its codes)
     hipEvent_t up_ev[4] = {};
     void *pin = nullptr;   // pinned host staging
     size_t pin_cap = 0;
@@ -163,8 +164,10 @@ int grow_pinned(size_t bytes) {
 // Allocates a resident weight, lets fill() put the row-major e4m3 codes into
 // the device staging buffer raw and the fp32 block scales into w.scale
 // (asynchronously on st), then repacks raw into the lane-order tiles.
+// Allocates a resident weight and lets fill() write its lane-order tiles
+// and fp32 block scales (asynchronously on st); synchronises st.
 template <typename Fill>
-int weight_build(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
+int weight_alloc_fill(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
     if (!out) return set_error(Q35MM_EINVAL, "null argument");
     if (rows == 0 || cols == 0) return set_error(Q35MM_EINVAL, "empty weight %ux%u", rows, cols);
     int rc = ensure_device();
@@ -177,11 +180,8 @@ int weight_build(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
     h->w.kb = kb;
     const size_t tiled_bytes = (size_t)nb * kb * kBlockBytes;
     const size_t scale_bytes = (size_t)nb * kb * sizeof(float);
-    const size_t raw_bytes = (size_t)rows * cols;
-    uint8_t *raw = nullptr;
     auto fail = [&](int code) {
         (void)hipStreamSynchronize(g_dev.stream);
-        if (raw) (void)hipFree(raw);
         if (h->w.codes) (void)hipFree(h->w.codes);
         if (h->w.scale) (void)hipFree(h->w.scale);
         delete h;
@@ -195,20 +195,37 @@ int weight_build(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
         h->w.scale = nullptr;
         return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for scales failed", scale_bytes));
     }
-    if (hipMalloc(&raw, raw_bytes) != hipSuccess) {
-        raw = nullptr;
-        return fail(set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for staging failed", raw_bytes));
-    }
     hipStream_t st = g_dev.stream;
-    rc = fill(h->w, raw, st);
+    rc = fill(h->w, st);
     if (rc) return fail(rc);
-    if (launch_repack(raw, rows, cols, nb, kb, h->w.codes, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+    if (hipStreamSynchronize(st) != hipSuccess)
         return fail(set_error(Q35MM_EHIP, "weight upload failed: %s", hipGetErrorString(hipGetLastError())));
-    (void)hipFree(raw);
-    raw = nullptr;
     h->bytes = tiled_bytes + scale_bytes;
     *out = h;
     return Q35MM_OK;
+}
+
+// As weight_alloc_fill, with fill() writing row-major e4m3 codes into a
+// device staging buffer raw, which is then repacked into the tiles.
+template <typename Fill>
+int weight_build(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fill) {
+    uint8_t *raw = nullptr;
+    const size_t raw_bytes = (size_t)rows * cols;
+    const int rc = weight_alloc_fill(rows, cols, out, [&](Weight &w, hipStream_t st) -> int {
+        if (hipMalloc(&raw, raw_bytes) != hipSuccess) {
+            raw = nullptr;
+            return set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for staging failed", raw_bytes);
+        }
+        int r = fill(w, raw, st);
+        if (r) return r;
+        HIP_TRY(launch_repack(raw, rows, cols, w.nb, w.kb, w.codes, st));
+        return Q35MM_OK;
+    });
+    if (raw) {
+        (void)hipStreamSynchronize(g_dev.stream);
+        (void)hipFree(raw);
+    }
+    return rc;
 }
 
 int weight_create(const uint8_t *W, const float *scale_f32_rowmajor, uint32_t rows, uint32_t cols,
@@ -381,7 +398,6 @@ int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hi
 // ---------------------------------------------------------------------
 constexpr size_t kUpChunk = 16u << 20;   // bytes per pinned chunk
 constexpr int kUpBufs = 4;
-constexpr int kUpReaders = 4;            // threads reading one chunk from the file
 
 int upload_ring() {
     for (int i = 0; i < kUpBufs; i++) {
@@ -390,48 +406,83 @@ int upload_ring() {
             g_dev.up_pin[i] = nullptr;
             return set_error(Q35MM_ENOMEM, "hipHostMalloc(%zu) for the upload ring failed", kUpChunk);
         }
+        if (hipMalloc(&g_dev.up_dev[i], kUpChunk + kUpChunk / 2) != hipSuccess) {
+            g_dev.up_dev[i] = nullptr;
+            return set_error(Q35MM_ENOMEM, "hipMalloc for the upload ring failed");
+        }
         HIP_TRY(hipEventCreateWithFlags(&g_dev.up_ev[i], hipEventDisableTiming));
+    }
+    for (int i = 0; i < kUpBufs; i++) HIP_TRY(hipEventSynchronize(g_dev.up_ev[i]));
+    return Q35MM_OK;
+}
+
+// Streams bytes [0, t.bytes) of tensor t through the ring in pieces of at
+// most piece bytes (a multiple of the tensor's row size for the callers
+// below): piece i is read from the file into pinned slot i % 4 (reader
+// threads), copied to the device slot, and handed to
+// consume(i, offset, bytes, device slot) on st; a slot is reused once the
+// work queued after it has finished.
+template <typename Consume>
+int stream_tensor(const st::Archive &a, const st::Tensor &t, uint64_t piece, hipStream_t st, Consume consume) {
+    int rc = upload_ring();
+    if (rc) return rc;
+    size_t i = 0;
+    for (uint64_t off = 0; off < t.bytes; off += piece, i++) {
+        const int b = (int)(i % kUpBufs);
+        if (i >= (size_t)kUpBufs) HIP_TRY(hipEventSynchronize(g_dev.up_ev[b]));
+        const uint64_t len = std::min<uint64_t>(piece, t.bytes - off);
+        if (!a.read_parallel(t, off, len, g_dev.up_pin[b]))
+            return set_error(Q35MM_EIO, "read of %s (%llu bytes at %llu) failed", t.name.c_str(),
+                             (unsigned long long)len, (unsigned long long)off);
+        HIP_TRY(hipMemcpyAsync(g_dev.up_dev[b], g_dev.up_pin[b], len, hipMemcpyHostToDevice, st));
+        rc = consume(i, off, len, static_cast<uint8_t *>(g_dev.up_dev[b]));
+        if (rc) return rc;
+        HIP_TRY(hipEventRecord(g_dev.up_ev[b], st));
     }
     return Q35MM_OK;
 }
 
-// Tensor bytes [0, t.bytes) -> device dst, asynchronously on st: the file is
-// read in 16 MiB chunks (kUpReaders threads per chunk) into a ring of pinned
-// buffers, each copied to HBM while the next one is read.  Complete once st
-// is synchronised.
+// Whole tensor -> device dst (no conversion).
 int upload_tensor(const st::Archive &a, const st::Tensor &t, void *dst, hipStream_t st) {
-    int rc = upload_ring();
-    if (rc) return rc;
-    for (int i = 0; i < kUpBufs; i++) HIP_TRY(hipEventSynchronize(g_dev.up_ev[i]));
     uint8_t *d = static_cast<uint8_t *>(dst);
-    size_t i = 0;
-    for (uint64_t off = 0; off < t.bytes; off += kUpChunk, i++) {
-        const int b = (int)(i % kUpBufs);
-        if (i >= (size_t)kUpBufs) HIP_TRY(hipEventSynchronize(g_dev.up_ev[b]));
-        const uint64_t len = std::min<uint64_t>(kUpChunk, t.bytes - off);
-        uint8_t *pin = static_cast<uint8_t *>(g_dev.up_pin[b]);
-        bool ok = true;
-        if (len >= (4u << 20)) {
-            const uint64_t part = (len / kUpReaders + 4095) & ~(uint64_t)4095;
-            bool oks[kUpReaders];
-            std::thread th[kUpReaders - 1];
-            auto rd = [&](int k) {
-                const uint64_t o = std::min<uint64_t>(len, part * k), e = std::min<uint64_t>(len, o + part);
-                oks[k] = e <= o || a.read(t, off + o, e - o, pin + o);
-            };
-            for (int k = 1; k < kUpReaders; k++) th[k - 1] = std::thread(rd, k);
-            rd(0);
-            for (auto &x : th) x.join();
-            for (bool o : oks) ok = ok && o;
-        } else {
-            ok = a.read(t, off, len, pin);
-        }
-        if (!ok) return set_error(Q35MM_EIO, "read of %s (%llu bytes at %llu) failed", t.name.c_str(),
-                                  (unsigned long long)len, (unsigned long long)off);
-        HIP_TRY(hipMemcpyAsync(d + off, pin, len, hipMemcpyHostToDevice, st));
-        HIP_TRY(hipEventRecord(g_dev.up_ev[b], st));
-    }
-    return Q35MM_OK;
+    return stream_tensor(a, t, kUpChunk, st, [&](size_t, uint64_t off, uint64_t len, uint8_t *src) -> int {
+        HIP_TRY(hipMemcpyAsync(d + off, src, len, hipMemcpyDeviceToDevice, st));
+        return Q35MM_OK;
+    });
+}
+
+// Rows per piece for a tensor of row_bytes bytes per row: whole 128-row
+// groups, as many as fit a chunk (0 if one group does not fit).
+uint64_t group_rows_per_piece(uint64_t row_bytes) {
+    const uint64_t groups = kUpChunk / (128 * row_bytes);
+    return groups * 128;
+}
+
+// F8_E4M3 [rows][cols] tensor -> the lane-order tiles of w, piece by piece:
+// each piece is whole 128-row groups, which are contiguous in the tiles.
+int upload_fp8_tiled(const st::Archive &a, const st::Tensor &t, Weight &w, hipStream_t st) {
+    const uint64_t prow = group_rows_per_piece(w.cols);
+    return stream_tensor(a, t, prow * w.cols, st, [&](size_t, uint64_t off, uint64_t len, uint8_t *src) -> int {
+        const uint32_t r0 = (uint32_t)(off / w.cols), n = (uint32_t)(len / w.cols);
+        uint8_t *dst = w.codes + (size_t)(r0 / kBlock) * w.kb * kBlockBytes;
+        HIP_TRY(launch_repack(src, n, w.cols, (n + kBlock - 1) / kBlock, w.kb, dst, st));
+        return Q35MM_OK;
+    });
+}
+
+// BF16 [rows][cols] tensor -> quantized codes (tiles of w) and fp32 scales,
+// piece by piece (whole 128-row groups, which quantize independently).
+int upload_bf16_quantized(const st::Archive &a, const st::Tensor &t, Weight &w, hipStream_t st) {
+    const uint64_t prow = group_rows_per_piece((uint64_t)w.cols * 2);
+    return stream_tensor(a, t, prow * w.cols * 2, st, [&](size_t, uint64_t off, uint64_t len, uint8_t *src) -> int {
+        const uint32_t r0 = (uint32_t)(off / ((uint64_t)w.cols * 2)), n = (uint32_t)(len / ((uint64_t)w.cols * 2));
+        const uint32_t g0 = r0 / kBlock, ng = (n + kBlock - 1) / kBlock;
+        uint8_t *codes = src + kUpChunk;   // the slot's spare half
+        HIP_TRY(launch_quantize_bf16(reinterpret_cast<const uint16_t *>(src), n, w.cols, codes, nullptr,
+                                     w.scale + (size_t)g0 * w.kb, st));
+        HIP_TRY(launch_repack(codes, n, w.cols, ng, w.kb, w.codes + (size_t)g0 * w.kb * kBlockBytes, st));
+        return Q35MM_OK;
+    });
 }
 
 // The reference loader's strict lookup (qwen35-c/src/q35_model.c:225-249):
@@ -465,6 +516,11 @@ int st_load_fp8(const st::Archive &a, const char *name, uint32_t rows, uint32_t 
     std::vector<uint16_t> sc((size_t)sshape[0] * sshape[1]);
     if (!a.read(*ts, 0, ts->bytes, sc.data())) return set_error(Q35MM_EIO, "read of %s failed", sname.c_str());
     const std::vector<float> f = widen_scales(sc.data(), rows, cols);
+    if (group_rows_per_piece(cols) > 0)
+        return weight_alloc_fill(rows, cols, out, [&](Weight &w, hipStream_t st) -> int {
+            HIP_TRY(hipMemcpyAsync(w.scale, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice, st));
+            return upload_fp8_tiled(a, *tw, w, st);
+        });
     return weight_build(rows, cols, out, [&](Weight &w, uint8_t *raw, hipStream_t st) -> int {
         HIP_TRY(hipMemcpyAsync(w.scale, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice, st));
         return upload_tensor(a, *tw, raw, st);
@@ -483,6 +539,9 @@ int st_load_ab(const st::Archive &a, const char *name, uint32_t rows, uint32_t c
     const uint32_t wshape[2] = {rows, cols};
     int rc = need_tensor(a, name, st::kBF16, 2, wshape, &t);
     if (rc) return rc;
+    if (group_rows_per_piece((uint64_t)cols * 2) > 0)
+        return weight_alloc_fill(rows, cols, out,
+                                 [&](Weight &w, hipStream_t st) { return upload_bf16_quantized(a, *t, w, st); });
     uint16_t *src = nullptr;
     rc = weight_build(rows, cols, out, [&](Weight &w, uint8_t *raw, hipStream_t st) -> int {
         if (hipMalloc(&src, t->bytes) != hipSuccess) {
@@ -1144,8 +1203,10 @@ Q35MM_API void q35mm_shutdown(void) {
     g_dev.pin_cap = 0;
     for (int i = 0; i < 4; i++) {
         if (g_dev.up_pin[i]) (void)hipHostFree(g_dev.up_pin[i]);
+        if (g_dev.up_dev[i]) (void)hipFree(g_dev.up_dev[i]);
         if (g_dev.up_ev[i]) (void)hipEventDestroy(g_dev.up_ev[i]);
         g_dev.up_pin[i] = nullptr;
+        g_dev.up_dev[i] = nullptr;
         g_dev.up_ev[i] = nullptr;
     }
     if (g_dev.stream) (void)hipStreamDestroy(g_dev.stream);

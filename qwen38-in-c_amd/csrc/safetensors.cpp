@@ -9,8 +9,12 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
 #include <memory>
+#include <mutex>
+#include <thread>
 
 namespace q35mm {
 namespace st {
@@ -297,7 +301,85 @@ bool read_full(int fd, uint64_t off, uint64_t len, void *dst) {
     return true;
 }
 
+// Persistent reader threads: run(n, fn) calls fn(0..n-1) on the workers
+// and the caller and returns when all calls are done.  Never destroyed (its
+// idle threads end with the process).
+class ReadPool {
+  public:
+    static ReadPool &get() {
+        static ReadPool *p = new ReadPool();
+        return *p;
+    }
+
+    void run(int n, const std::function<void(int)> &fn) {
+        std::lock_guard<std::mutex> one(run_mu_);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            fn_ = &fn;
+            n_ = n;
+            next_ = 0;
+            done_ = 0;
+            gen_++;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return done_ == n_; });
+        fn_ = nullptr;
+    }
+
+  private:
+    static constexpr int kWorkers = 3;
+
+    ReadPool() {
+        for (int i = 0; i < kWorkers; i++)
+            std::thread([this] {
+                uint64_t seen = 0;
+                for (;;) {
+                    {
+                        std::unique_lock<std::mutex> lk(mu_);
+                        cv_.wait(lk, [&] { return gen_ != seen; });
+                        seen = gen_;
+                    }
+                    work();
+                }
+            }).detach();
+    }
+
+    void work() {
+        std::unique_lock<std::mutex> lk(mu_);
+        while (fn_ && next_ < n_) {
+            const int k = next_++;
+            const std::function<void(int)> *fn = fn_;
+            lk.unlock();
+            (*fn)(k);
+            lk.lock();
+            if (++done_ == n_) done_cv_.notify_all();
+        }
+    }
+
+    std::mutex run_mu_, mu_;
+    std::condition_variable cv_, done_cv_;
+    const std::function<void(int)> *fn_ = nullptr;
+    int n_ = 0, next_ = 0, done_ = 0;
+    uint64_t gen_ = 0;
+};
+
 }  // namespace
+
+bool Archive::read_parallel(const Tensor &t, uint64_t off, uint64_t len, void *dst) const {
+    constexpr uint64_t kPart = 2u << 20;   // bytes per reader call
+    if (len <= kPart) return read(t, off, len, dst);
+    const int n = (int)((len + kPart - 1) / kPart);
+    std::vector<char> ok((size_t)n, 0);
+    ReadPool::get().run(n, [&](int k) {
+        const uint64_t o = (uint64_t)k * kPart, e = std::min(len, o + kPart);
+        ok[(size_t)k] = read(t, off + o, e - o, static_cast<uint8_t *>(dst) + o) ? 1 : 0;
+    });
+    for (char c : ok)
+        if (!c) return false;
+    return true;
+}
 
 Archive::~Archive() {
     for (int fd : fds)

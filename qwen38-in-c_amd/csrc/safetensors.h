@@ -55,6 +55,9 @@ struct Archive {
     const Tensor *find(const char *name) const;
     // bytes [off, off + len) of tensor t into dst; false on a short read
     bool read(const Tensor &t, uint64_t off, uint64_t len, void *dst) const;
+    // the same, split over a small pool of reader threads (page-cache reads
+    // run at several times one thread's rate)
+    bool read_parallel(const Tensor &t, uint64_t off, uint64_t len, void *dst) const;
 
   private:
     int index_file(const std::string &path, uint32_t file, std::string &msg);
