@@ -245,6 +245,52 @@ def bench_upload(q, wl, base, reps: int = 3):
         os.rmdir(tmp)
 
 
+def bench_stragglers(q, wl, torch, dev, use_graph: bool, n: int = 512):
+    """The reference's prefill calls DeltaNet out_proj and attention o_proj
+    (both 6144 -> 5120) once per token (qwen35-c/src/q35_deltanet.c:498,
+    qwen35-c/src/q35_attn.c:262).  Time n per-token calls against one batch
+    call, on device pointers and through the host-pointer ABI."""
+    import numpy as np
+    k, nrows = 6144, 5120
+    W, sc = wl.gen_weight(wl.SEED_BASE + 8, nrows, k)
+    w = q.Weight(W, sc)
+    X = wl.gen_act(wl.SEED_BASE + 9, n, k)
+    dX = torch.from_numpy(X).to(dev)
+    dY = torch.empty((n, nrows), device=dev)
+
+    def per_token(_i):
+        for t in range(n):
+            q.gemv(w, dX[t:t + 1], dY[t:t + 1], m=1)
+
+    def batched(_i):
+        q.matmul(w, dX, dY)
+    el_t, g1 = time_graph(torch, per_token, 1, 1, use_graph)
+    del g1
+    el_b, g2 = time_graph(torch, batched, 5, 2, use_graph)
+    del g2
+    Yh = np.empty((n, nrows), np.float32)
+    q.mm_fp8_batch(W, sc, X)   # resident copy made, warm
+    t0 = time.perf_counter()
+    for t in range(n):
+        Yh[t] = q.mm_fp8(W, sc, X[t])
+    t1 = time.perf_counter()
+    Yb = q.mm_fp8_batch(W, sc, X)
+    t2 = time.perf_counter()
+    rel = float(np.linalg.norm(Yb.astype(np.float64) - Yh) / np.linalg.norm(Yh.astype(np.float64)))
+    q.release(W)
+    w.free()
+    flops = 2.0 * n * k * nrows
+    return {"shape": f"{k}->{nrows}", "tokens": n,
+            "device_per_token_ms": round(el_t * 1e3, 3), "device_batched_ms": round(el_b / 5 * 1e3, 3),
+            "device_speedup": round(el_t / (el_b / 5), 1),
+            "device_batched_TFLOPs": round(flops / (el_b / 5) / 1e12, 1),
+            "host_abi_per_token_ms": round((t1 - t0) * 1e3, 2), "host_abi_batched_ms": round((t2 - t1) * 1e3, 2),
+            "batched_vs_per_token_rel_l2": rel,
+            "note": "per-token = n q35_mm_fp8 / q35mm_gemv(m=1) calls (fp32 GEMV); batched = one "
+                    "q35_mm_fp8_batch / q35mm_matmul(m=n) call (bf16 GEMM at n >= 64; Q35MM_GEMM_MIN_M=0 keeps "
+                    "it on the GEMV, bitwise equal to per-token)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +304,8 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-mlp", dest="mlp", action="store_false",
                     help="skip the MLP block (RMSNorm, gate/up, SwiGLU, down, residual) at M=1")
+    ap.add_argument("--no-stragglers", dest="stragglers", action="store_false",
+                    help="skip per-token vs batched out_proj/o_proj at 512 tokens")
     ap.add_argument("--no-upload", dest="upload", action="store_false",
                     help="skip the safetensors -> HBM load of one layer")
     ap.add_argument("--no-lm-head", dest="lm_head", action="store_false",
@@ -470,6 +518,12 @@ def main():
         log(f"lm_head: {lm_head}")
         del gh, pool2
 
+    # ---- prefill stragglers: per-token out_proj / o_proj vs one batch ----
+    stragglers = None
+    if args.stragglers:
+        stragglers = bench_stragglers(q, wl, torch, dev, not args.eager)
+        log(f"stragglers: {stragglers}")
+
     # ---- checkpoint -> HBM: one layer's FP8 weights from a safetensors file ----
     upload = None
     if args.upload:
@@ -503,6 +557,7 @@ def main():
         "lm_head_bf16": lm_head,
         "mlp_block": mlp_out,
         "upload": upload,
+        "prefill_stragglers": stragglers,
     }
     print(json.dumps(out), flush=True)
 
