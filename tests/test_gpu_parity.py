@@ -375,3 +375,42 @@ def test_bf16_gemv_device_api_lm_head_rows(q, oracle, wl, gpu):
     q.bf16_gemv(dW, dx, dy)
     torch.cuda.synchronize()
     assert (dy.cpu().numpy().view(np.uint32) == oracle.mm_bf16(W, x).view(np.uint32)).all()
+
+
+def test_host_abi_from_several_threads(q, wl, gpu):
+    """The drop-in calls are serialised by the library lock: four host
+    threads calling q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4 at once
+    on shared and private weights get the bits of the same calls made one at
+    a time."""
+    import threading
+    Ws = [wl.gen_weight(200 + i, 640 + 128 * i, 1024) for i in range(3)]
+    Xs = [wl.gen_act(210 + i, 1 + i, 1024) for i in range(4)]
+    want = {}
+    for i, X in enumerate(Xs):
+        for j, (W, sc) in enumerate(Ws):
+            want[(i, j)] = q.mm_fp8_batch(W, sc, X)
+    errors = []
+
+    def worker(i):
+        try:
+            for rep in range(6):
+                j = (i + rep) % 3
+                W, sc = Ws[j]
+                got = q.mm_fp8_batch(W, sc, Xs[i]) if rep % 2 else np.stack(
+                    [q.mm_fp8(W, sc, x) for x in Xs[i]])
+                if not (got.view(np.uint32) == want[(i, j)].view(np.uint32)).all():
+                    errors.append((i, rep, j))
+            ys = q.mm_fp8_multi4([Ws[0][0], Ws[1][0]], [Ws[0][1], Ws[1][1]], Xs[i][0])
+            for j in range(2):
+                if not (ys[j].view(np.uint32) == want[(i, j)][0].view(np.uint32)).all():
+                    errors.append((i, "multi4", j))
+        except Exception as e:   # surfaced below
+            errors.append((i, repr(e)))
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors
+    for W, _ in Ws:
+        q.release(W)
