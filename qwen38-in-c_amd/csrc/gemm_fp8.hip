@@ -100,8 +100,7 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
                     if (col + e < k) v[e] = xp[e];
             }
         }
-        u32x2_t w = {f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16),
-                     f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16)};
+        u32x2_t w = {f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3])};
         *reinterpret_cast<u32x2_t *>(&t[r][c4 * 4]) = w;
     }
     __syncthreads();

@@ -57,8 +57,12 @@ __device__ __forceinline__ u32x4_t ld16(const uint8_t *p) {
 // block (b0 + i) mod KB:
 //   byte offset(c, q, ai, h) = (((c*2 + q) * R + ai) * 2 + h) * 16
 // where c = i*4 + chunk, q selects the first or second MFMA of the chunk,
-// ai = part*m + t, R = 3m, h = lane/32, and the 16 bytes hold columns
-// kb*128 + chunk*32 + 16h + 8q + (0..7).
+// ai = part*m + t, R = 3m rounded up to odd, h = lane/32, and the 16 bytes
+// hold columns
+// kb*128 + chunk*32 + 16h + 8q + (0..7).  An odd R keeps the 16 (c, q, h)
+// positions of one K block in 16 different 16-byte bank groups (an even R
+// puts a 256-byte multiple between consecutive (c, q) and the staging
+// writes of a wavefront pile onto two bank groups).
 //
 // Work item v (< m * nblk * 16) is one 8-column vector of one token.  The
 // loads of a thread's first kStagePre items are split from the rest so they
@@ -126,15 +130,15 @@ __device__ __forceinline__ void stage_finish(float (&xv)[8], const StageIn<XM> &
 }
 
 __device__ __forceinline__ void stage_store(uint8_t *lds, uint32_t m, const StageItem &it, const float (&xv)[8]) {
-    const uint32_t R = 3 * m;
-    uint32_t p0[8], p1[8], p2[8];
+    const uint32_t R = stage_rows(m);
+    uint32_t p0[4], p1[4], p2[4];   // packed pairs of columns
 #pragma unroll
-    for (int e = 0; e < 8; e++) split3_bf16(xv[e], p0[e], p1[e], p2[e]);
+    for (int e = 0; e < 4; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], p0[e], p1[e], p2[e]);
     const uint32_t c = it.kk >> 5, h = (it.kk >> 4) & 1, q = (it.kk >> 3) & 1;
     const uint32_t base = (c * 2 + q) * R;
-    u32x4_t w0 = {p0[0] | (p0[1] << 16), p0[2] | (p0[3] << 16), p0[4] | (p0[5] << 16), p0[6] | (p0[7] << 16)};
-    u32x4_t w1 = {p1[0] | (p1[1] << 16), p1[2] | (p1[3] << 16), p1[4] | (p1[5] << 16), p1[6] | (p1[7] << 16)};
-    u32x4_t w2 = {p2[0] | (p2[1] << 16), p2[2] | (p2[3] << 16), p2[4] | (p2[5] << 16), p2[6] | (p2[7] << 16)};
+    const u32x4_t w0 = {p0[0], p0[1], p0[2], p0[3]};
+    const u32x4_t w1 = {p1[0], p1[1], p1[2], p1[3]};
+    const u32x4_t w2 = {p2[0], p2[1], p2[2], p2[3]};
     *reinterpret_cast<u32x4_t *>(lds + ((base + 0 * m + it.t) * 2 + h) * 16) = w0;
     *reinterpret_cast<u32x4_t *>(lds + ((base + 1 * m + it.t) * 2 + h) * 16) = w1;
     *reinterpret_cast<u32x4_t *>(lds + ((base + 2 * m + it.t) * 2 + h) * 16) = w2;
@@ -250,7 +254,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     const uint32_t mrow = lane & 31, hh = lane >> 5;
     const uint32_t tt = mrow & 7, pp = mrow >> 3;  // A row = token + 8*part
     const bool a_active = (tt < M) && (pp < 3);
-    const uint32_t R = 3 * M;
+    const uint32_t R = stage_rows(M);
     // A-operand address = a_base + (chunk*2 + q) * a_step.  Rows that carry
     // no token (t >= m, or the unused rows 24..31) read a 16-byte zero slot
     // placed after the stage, so every lane issues the same LDS read.
@@ -501,7 +505,7 @@ uint32_t gemv_max_contrib(uint32_t nblocks, uint32_t nctas, uint32_t kb) {
 }
 
 size_t gemv_lds_bytes(uint32_t m, uint32_t range_blocks) {
-    return (size_t)range_blocks * kBlock * 3 * m * 2 + 16;   // + zero slot
+    return (size_t)range_blocks * 256 * stage_rows(m) + 16;   // + zero slot
 }
 
 bool gemv_norm_fits(uint32_t m, uint32_t k) {

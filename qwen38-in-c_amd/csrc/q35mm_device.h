@@ -87,24 +87,32 @@ __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8_cvt(uint32_t w0, uint32_t w
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t u = f32_bits(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 (a in the low half), round to nearest even: one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float a, float b) {
+    const f32x2v_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return bits_f32(b << 16); }
 
-// Exact three-way split of an fp32 into bf16 parts: x == p0 + p1 + p2 for
-// every normal x (each residual is exact in fp32 and has at most 16, then 8,
-// significant bits).
-__device__ __forceinline__ void split3_bf16(float x, uint32_t &p0, uint32_t &p1, uint32_t &p2) {
-    p0 = f32_to_bf16_rne(x);
-    float r1 = x - bf16_to_f32(p0);
-    p1 = f32_to_bf16_rne(r1);
-    float r2 = r1 - bf16_to_f32(p1);
-    p2 = f32_to_bf16_rne(r2);
+// Exact three-way split of two fp32 values into bf16 parts, packed in pairs:
+// x == p0 + p1 + p2 for every normal x (each residual is exact in fp32 and has
+// at most 16, then 8, significant bits).  Each part is a round-to-nearest-even
+// conversion; about 5.5 instructions per value.
+__device__ __forceinline__ void split3_bf16x2(float a, float b, uint32_t &p0, uint32_t &p1, uint32_t &p2) {
+#pragma clang fp contract(off)
+    const f32x2v_t x = {a, b};
+    const bf16x2v_t b0 = __builtin_convertvector(x, bf16x2v_t);
+    const f32x2v_t r1 = x - __builtin_convertvector(b0, f32x2v_t);
+    const bf16x2v_t b1 = __builtin_convertvector(r1, bf16x2v_t);
+    const f32x2v_t r2 = r1 - __builtin_convertvector(b1, f32x2v_t);
+    p0 = __builtin_bit_cast(uint32_t, b0);
+    p1 = __builtin_bit_cast(uint32_t, b1);
+    p2 = __builtin_bit_cast(uint32_t, __builtin_convertvector(r2, bf16x2v_t));
 }
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {

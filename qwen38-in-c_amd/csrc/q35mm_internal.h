@@ -81,6 +81,10 @@ struct GemvParams {
     uint32_t x_vec;      // x 16-byte aligned, ldx % 4 == 0, k % 8 == 0: vector staging loads
 };
 
+// A-operand rows of the GEMV's staged activations: token x bf16 part (3m),
+// rounded up to an odd count for conflict-free LDS staging writes.
+__host__ __device__ constexpr uint32_t stage_rows(uint32_t m) { return (3 * m) | 1u; }
+
 // P for T blocks on a device with cus compute units; depends only on the
 // weight shape, so a batch of m tokens gives exactly the bits of m single
 // calls.
