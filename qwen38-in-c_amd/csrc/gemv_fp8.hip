@@ -70,6 +70,7 @@ __device__ __forceinline__ u32x4_t ld16(const uint8_t *p) {
 // order, so anything issued before the weights can be waited for without
 // waiting for the weights.
 constexpr uint32_t kStagePre = 2;
+constexpr uint32_t kStageBatch = 4;
 
 struct StageItem {
     uint32_t t, kk, kg;   // token, slot-relative column, global column
@@ -89,8 +90,9 @@ __device__ __forceinline__ StageItem stage_item(uint32_t i, uint32_t per_t, uint
 // (vec: two 16-byte loads; the row is 16-byte aligned and k % 8 == 0) or
 // min(kg + e, k - 1) (eight 4-byte loads).  Unconditional, so no branch sits
 // between them and the weight prologue; columns >= k are zeroed later.
-__device__ __forceinline__ void load8(float (&v)[8], const float *row, uint32_t kg, uint32_t k, bool vec) {
-    if (vec) {
+template <bool VEC>
+__device__ __forceinline__ void load8(float (&v)[8], const float *row, uint32_t kg, uint32_t k) {
+    if constexpr (VEC) {
         const float4 *q = reinterpret_cast<const float4 *>(row + min(kg, k - 8));
         const float4 a = q[0], b = q[1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
@@ -109,11 +111,11 @@ struct StageIn {
     float a[8];
 };
 
-template <uint32_t XM>
-__device__ __forceinline__ void stage_load(StageIn<XM> &in, const GemvParams &p, const StageItem &it, bool vec) {
-    load8(in.x, p.x + (size_t)it.t * p.ldx, it.kg, p.k, vec);
-    if constexpr (XM == kXSwiGLU) load8(in.a, p.x2 + (size_t)it.t * p.ldx, it.kg, p.k, vec);
-    if constexpr (XM == kXRmsNorm) load8(in.a, p.norm_w, it.kg, p.k, vec);
+template <uint32_t XM, bool VEC>
+__device__ __forceinline__ void stage_load(StageIn<XM> &in, const GemvParams &p, const StageItem &it) {
+    load8<VEC>(in.x, p.x + (size_t)it.t * p.ldx, it.kg, p.k);
+    if constexpr (XM == kXSwiGLU) load8<VEC>(in.a, p.x2 + (size_t)it.t * p.ldx, it.kg, p.k);
+    if constexpr (XM == kXRmsNorm) load8<VEC>(in.a, p.norm_w, it.kg, p.k);
 }
 
 // The staged values: the transform of the raw inputs, columns >= k zeroed.
@@ -228,7 +230,7 @@ __device__ __forceinline__ void norm_finish(const GemvParams &p, const float *sq
 
 }  // namespace
 
-template <uint32_t XM>
+template <uint32_t XM, bool VEC>
 __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t s_ticket;
@@ -282,12 +284,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     // ---- prologue: activation loads, then the first weight blocks ----
     const uint32_t per_t = nblk * 16;
     const uint32_t nvec = M * per_t;
-    const bool vec = p.x_vec != 0;
     StageIn<XM> xpre[kStagePre];
     auto stage_pre_load = [&]() {
 #pragma unroll
         for (uint32_t u = 0; u < kStagePre; u++)   // index clamped: loads are unconditional
-            stage_load(xpre[u], p, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0), vec);
+            stage_load<XM, VEC>(xpre[u], p, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0));
     };
     auto ring_prologue = [&]() {
 #pragma unroll
@@ -324,13 +325,24 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
         stage_finish(xv, xpre[u], p.k, it, s_inv);
         if (i < nvec) stage_store(lds, M, it, xv);
     }
-    for (uint32_t i = threadIdx.x + kStagePre * kGemvThreads; i < nvec; i += kGemvThreads) {
-        const StageItem it = stage_item(i, per_t, KB, b0);
-        StageIn<XM> in;
-        stage_load(in, p, it, vec);
-        float xv[8];
-        stage_finish(xv, in, p.k, it, s_inv);
-        stage_store(lds, M, it, xv);
+    // The rest (m > 1) in batches of kStageBatch items per thread: the loads
+    // of a batch are all issued before any is used (the scheduling barrier
+    // keeps the compiler from sinking them to their uses), one memory round
+    // trip per batch.
+    for (uint32_t i0 = threadIdx.x + kStagePre * kGemvThreads; i0 < nvec; i0 += kStageBatch * kGemvThreads) {
+        StageIn<XM> in[kStageBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kStageBatch; u++)   // index clamped: loads are unconditional
+            stage_load<XM, VEC>(in[u], p, stage_item(min(i0 + u * kGemvThreads, nvec - 1), per_t, KB, b0));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t u = 0; u < kStageBatch; u++) {
+            const uint32_t i = i0 + u * kGemvThreads;
+            const StageItem it = stage_item(min(i, nvec - 1), per_t, KB, b0);
+            float xv[8];
+            stage_finish(xv, in[u], p.k, it, s_inv);
+            if (i < nvec) stage_store(lds, M, it, xv);
+        }
     }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + zero_off)[threadIdx.x] = 0u;
     __syncthreads();
@@ -520,8 +532,9 @@ size_t gemv_norm_lds_bytes(uint32_t m, uint32_t norm_cols) {
 
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream) {
     using Kernel = void (*)(GemvParams);
-    static const Kernel kernels[3] = {gemv_fp8_kernel<kXPlain>, gemv_fp8_kernel<kXRmsNorm>,
-                                      gemv_fp8_kernel<kXSwiGLU>};
+    static const Kernel kernels[6] = {gemv_fp8_kernel<kXPlain, false>,   gemv_fp8_kernel<kXRmsNorm, false>,
+                                      gemv_fp8_kernel<kXSwiGLU, false>,  gemv_fp8_kernel<kXPlain, true>,
+                                      gemv_fp8_kernel<kXRmsNorm, true>,  gemv_fp8_kernel<kXSwiGLU, true>};
     static bool attr_set = false;
     if (!attr_set) {
         for (Kernel k : kernels) {
@@ -538,7 +551,7 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t stream) {
         lds = std::max(lds, gemv_norm_lds_bytes(p.m, p.norm_cols));
     }
     if (lds > kGemvMaxLds) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kernels[p.xmode], dim3(p.nctas), dim3(kGemvThreads), lds, stream, p);
+    hipLaunchKernelGGL(kernels[p.xmode + (p.x_vec ? 3 : 0)], dim3(p.nctas), dim3(kGemvThreads), lds, stream, p);
     return hipGetLastError();
 }
 
