@@ -302,6 +302,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-blas", dest="blas", action="store_false",
+                    help="skip the vendor bf16 GEMM (torch.mm -> hipBLASLt) timed beside the prefill GEMM")
     ap.add_argument("--no-mlp", dest="mlp", action="store_false",
                     help="skip the MLP block (RMSNorm, gate/up, SwiGLU, down, residual) at M=1")
     ap.add_argument("--no-stragglers", dest="stragglers", action="store_false",
@@ -489,11 +491,29 @@ def main():
             log(f"prefill {name}: {tf:.1f} TFLOP/s")
             del gp
             w.free()
+            if args.blas:
+                # Context, not a baseline of the same op: the vendor library's
+                # plain bf16 x bf16 -> bf16 GEMM of the same shape (no fp8
+                # decode, no block scales, half the output bytes).
+                Wb = torch.randn((n, k), device=dev, dtype=torch.bfloat16)
+                Xb = X.to(torch.bfloat16)
+                Yb = torch.empty((512, n), device=dev, dtype=torch.bfloat16)
+
+                def call_blas(_i, Wb=Wb, Xb=Xb, Yb=Yb):
+                    torch.mm(Xb, Wb.t(), out=Yb)
+                el_b, gb = time_graph(torch, call_blas, args.prefill_reps, 2, not args.eager)
+                prefill[name]["hipblaslt_bf16_TFLOPs"] = round(wl.flops(512, k, n) * args.prefill_reps / el_b / 1e12, 1)
+                log(f"prefill {name}: hipBLASLt bf16 {prefill[name]['hipblaslt_bf16_TFLOPs']} TFLOP/s")
+                del gb, Wb, Xb, Yb
+            del X, Y
+            torch.cuda.empty_cache()
         tot_flops = sum(wl.flops(512, k, n) for _, k, n in wl.PREFILL_SHAPES)
         tot_us = sum(v["us"] for v in prefill.values())
         tf_all = tot_flops / (tot_us * 1e-6) / 1e12
         prefill["total"] = {"TFLOPs": round(tf_all, 1), "frac_of_bf16_peak": round(tf_all / BF16_PEAK_TFLOPS, 4),
-                            "note": "includes the fp32->bf16 activation prepass kernel of each call"}
+                            "note": "includes the fp32->bf16 activation prepass kernel of each call; "
+                                    "hipblaslt_bf16_TFLOPs = torch.mm of bf16 operands of the same shape "
+                                    "(bf16 output), for context"}
 
     # ---- BF16 lm_head matvec (q35_mm_bf16): 248320 x 5120 ----
     lm_head = None

@@ -1,0 +1,229 @@
+// gemv_rows.hip -- decode GEMV, m <= 8 tokens, row-split decomposition for
+// weights of a few thousand rows and a short K.
+//
+// Replaces the same hot loop as gemv_fp8.hip (qwen35-c/src/q35_mm.c:88-198,
+// mm_fp8_row under q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4) for
+// the shapes gemv_rows_shape() selects, e.g. 5120->6144 and 4096->5120.
+//
+// Decomposition.  One workgroup per 32-row sub-tile (the weight's
+// ceil(rows/32) sub-tiles fill between half and all of the CUs), and the
+// workgroup's kGemvRsWaves wavefronts split K into contiguous ranges of K
+// blocks.  Each wavefront streams its range of the sub-tile (4 KiB per K
+// block, one 16-byte load per lane per 1 KiB chunk) through a ring of
+// kRsDepth blocks; the wavefront partials are added through LDS in
+// wavefront order at the end.  No partial output leaves the workgroup, so
+// there are no tickets, no workspace and no second pass: that is the whole
+// point against stream-K, whose split-group protocol costs a few
+// microseconds per launch, as much as streaming these weights takes.
+//
+// Arithmetic is the stream-K kernel's: e4m3 -> bf16 exactly, activations
+// split exactly into three bf16 parts (A-operand rows m = token + 8*part),
+// v_mfma_f32_32x32x16_bf16 per K block, the block's fp32 scale applied with
+// one fmaf per output.  The summation order depends only on the shape (K
+// ranges per wavefront, wavefronts in order), so a batch of m tokens gives
+// exactly the bits of m single-token calls, and a weight gives the same
+// bits alone or in a multi-weight launch.
+//
+// Activations.  Each K block's activations ride the weight ring one block
+// ahead: the slot that brings the weights of block b brings the activations
+// of block b+1, which are split into the wavefront's second A-operand slot
+// in LDS while block b's MFMAs run.  Nothing is staged up front and no
+// barrier is needed before the stream: each wavefront only reads LDS it
+// wrote itself (LDS operations of one wavefront complete in order).
+#include "q35mm_device.h"
+#include "q35mm_internal.h"
+
+namespace q35mm {
+
+namespace {
+
+constexpr uint32_t kRsDepth = 4;   // K blocks in flight per wavefront
+
+// The activations of one K block for all m tokens: 8-column vector
+// v < 16m (token v/16, block columns (v%16)*8 ..) is the (v/64)-th vector
+// of lane v%64.  Loads are unconditional (token and columns clamped), so the
+// waits before each block stay static; stage_xblock masks what is not real.
+template <uint32_t NV>
+struct XBlock {
+    float v[NV][8];
+};
+
+template <bool VEC, uint32_t NV>
+__device__ __forceinline__ void load_xblock(XBlock<NV> &xb, const float *x, uint32_t ldx, uint32_t m, uint32_t k,
+                                            uint32_t kb, uint32_t lane) {
+#pragma unroll
+    for (uint32_t u = 0; u < NV; u++) {
+        const uint32_t v = min(lane + 64 * u, 16 * m - 1);
+        const uint32_t kg = kb * kBlock + (v & 15) * 8;
+        const float *row = x + (size_t)(v >> 4) * ldx;
+        if constexpr (VEC) {   // rows 16-byte aligned, k % 8 == 0
+            const float4 *q = reinterpret_cast<const float4 *>(row + min(kg, k - 8));
+            const float4 a = q[0], b = q[1];
+            xb.v[u][0] = a.x; xb.v[u][1] = a.y; xb.v[u][2] = a.z; xb.v[u][3] = a.w;
+            xb.v[u][4] = b.x; xb.v[u][5] = b.y; xb.v[u][6] = b.z; xb.v[u][7] = b.w;
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) xb.v[u][e] = row[min(kg + e, k - 1)];
+        }
+    }
+}
+
+// Split a block's activations into an A-operand slot of 256*R bytes:
+//   byte offset(c, q, ai, h) = (((c*2 + q) * R + ai) * 2 + h) * 16
+// for chunk c < 4, MFMA q < 2, A row ai = part*m + token, h = lane/32 of
+// the reading lane; the 16 bytes hold block columns c*32 + 16h + 8q + 0..7.
+// Columns >= k are staged as zero.
+template <uint32_t NV>
+__device__ __forceinline__ void stage_xblock(const XBlock<NV> &xb, uint8_t *slot, uint32_t m, uint32_t R, uint32_t k,
+                                             uint32_t kb, uint32_t lane) {
+#pragma unroll
+    for (uint32_t u = 0; u < NV; u++) {
+        const uint32_t v = lane + 64 * u;
+        if (v < 16 * m) {
+            const uint32_t t = v >> 4, kk = (v & 15) * 8, kg = kb * kBlock + kk;
+            float xv[8];
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) xv[e] = kg + e < k ? xb.v[u][e] : 0.0f;
+            uint32_t p0[4], p1[4], p2[4];
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], p0[e], p1[e], p2[e]);
+            const uint32_t c = kk >> 5, h = (kk >> 4) & 1, q = (kk >> 3) & 1;
+            const uint32_t base = (c * 2 + q) * R;
+            *reinterpret_cast<u32x4_t *>(slot + ((base + 0 * m + t) * 2 + h) * 16) = u32x4_t{p0[0], p0[1], p0[2], p0[3]};
+            *reinterpret_cast<u32x4_t *>(slot + ((base + 1 * m + t) * 2 + h) * 16) = u32x4_t{p1[0], p1[1], p1[2], p1[3]};
+            *reinterpret_cast<u32x4_t *>(slot + ((base + 2 * m + t) * 2 + h) * 16) = u32x4_t{p2[0], p2[1], p2[2], p2[3]};
+        }
+    }
+}
+
+}  // namespace
+
+// NV = 8-column activation vectors per lane and K block: 1 for m <= 4,
+// 2 for m <= 8.
+template <bool VEC, uint32_t NV>
+__global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[kGemvRsWaves][kGemvMaxM][kSubRows];
+
+    uint32_t si = 0;
+#pragma unroll
+    for (uint32_t i = 1; i < 4; i++)
+        if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
+    const GemvSeg &sg = p.seg[si];
+    const uint32_t sub = blockIdx.x - sg.cta_begin;   // 32-row sub-tile
+    const uint32_t g = sub >> 2, s = sub & 3;
+    const uint32_t KB = p.kb, M = p.m, R = stage_rows(M);
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t k0 = wv * KB / kGemvRsWaves, k1 = (wv + 1) * KB / kGemvRsWaves;   // KB >= waves
+
+    // This wavefront's LDS: two A-operand slots and a 16-byte zero slot.
+    // Lanes whose A row carries no token (t >= m, or rows 24..31) read the
+    // zero slot, so every lane issues the same LDS reads.
+    uint8_t *const wbase = lds + wv * gemv_rows_wave_lds(M);
+    const uint32_t mrow = lane & 31, hh = lane >> 5;
+    const uint32_t tt = mrow & 7, pp = mrow >> 3;
+    const bool a_active = tt < M && pp < 3;
+    const uint8_t *const arow = a_active ? wbase + ((pp * M + tt) * 2 + hh) * 16 : wbase + 512 * R;
+    const uint32_t a_slot = a_active ? 256 * R : 0;
+    const uint32_t a_step = a_active ? R * 32 : 0;
+    if (lane < 4) reinterpret_cast<uint32_t *>(wbase + 512 * R)[lane] = 0u;
+
+    // ---- ring: slot d holds the weights and scale of block b and the
+    // activations of block b+1 (clamped into the range) ----
+    const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
+    const float *scale = sg.scale + (size_t)g * KB;
+    u32x4_t buf[kRsDepth][4];
+    float scs[kRsDepth];
+    XBlock<NV> xr[kRsDepth];
+    auto load = [&](uint32_t d, uint32_t b) {
+        const uint8_t *src = codes + (size_t)b * kBlockBytes;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) buf[d][j] = *reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes);
+        scs[d] = scale[b];
+        load_xblock<VEC, NV>(xr[d], p.x, p.ldx, M, p.k, min(b + 1, k1 - 1), lane);
+    };
+    XBlock<NV> x0;
+    load_xblock<VEC, NV>(x0, p.x, p.ldx, M, p.k, k0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t d = 0; d + 1 < kRsDepth; d++) load(d, min(k0 + d, k1 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    stage_xblock<NV>(x0, wbase, M, R, p.k, k0, lane);   // waits for x0 only: loads complete in order
+
+    f32x16_t acc = {};
+    const f32x16_t zero = {};
+    for (uint32_t b = k0; b < k1; b += kRsDepth) {
+#pragma unroll
+        for (uint32_t d = 0; d < kRsDepth; d++) {
+            const uint32_t bb = b + d;
+            load((d + kRsDepth - 1) % kRsDepth, min(bb + kRsDepth - 1, k1 - 1));
+            // keep the scheduler from sinking these loads below block bb's math
+            __builtin_amdgcn_sched_barrier(0);
+            if (bb < k1) {
+                const uint32_t par = (bb - k0) & 1;
+                u32x4_t araw[8];
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++)
+                    araw[i] = *reinterpret_cast<const u32x4_t *>(arow + par * a_slot + i * a_step);
+                if (bb + 1 < k1) stage_xblock<NV>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, bb + 1, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                f32x16_t part;
+#pragma unroll
+                for (uint32_t j = 0; j < 4; j++)
+#pragma unroll
+                    for (uint32_t q = 0; q < 2; q++) {
+                        const bf16x8_t bop = e4m3x8_to_bf16x8(buf[d][j][2 * q], buf[d][j][2 * q + 1]);
+                        const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
+                        part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
+                    }
+                // rows 24..31 of the A operand carry nothing (regs 12..15)
+#pragma unroll
+                for (uint32_t r = 0; r < 12; r++) acc[r] = __builtin_fmaf(scs[d], part[r], acc[r]);
+            }
+        }
+    }
+
+    // ---- wavefront partials -> outputs, wavefronts added in order ----
+    // Lane (h, n) holds token 4h + r of row n in acc[r] (part 0), acc[r + 4]
+    // (part 1) and acc[r + 8] (part 2).
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++) {
+        const uint32_t t = 4 * hh + r;
+        if (t < M) red[wv][t][mrow] = (acc[r] + acc[r + 4]) + acc[r + 8];
+    }
+    __syncthreads();
+    if (threadIdx.x < kSubRows * M) {
+        const uint32_t t = threadIdx.x >> 5, n = threadIdx.x & 31;
+        float sum = red[0][t][n];
+#pragma unroll
+        for (uint32_t w = 1; w < kGemvRsWaves; w++) sum += red[w][t][n];
+        const uint32_t row = g * kBlock + s * kSubRows + n;
+        if (row < sg.rows) {
+            const size_t o = (size_t)t * sg.ldy + row;
+            sg.y[o] = sg.resid ? sg.resid[o] + sum : sum;
+        }
+    }
+}
+
+bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus) {
+    const uint32_t nsub = (rows + kSubRows - 1) / kSubRows;
+    return 2 * nsub >= cus && nsub <= cus && kb >= 2 * kGemvRsWaves && kb <= kGemvRsMaxKb;
+}
+
+uint32_t gemv_rows_ctas(uint32_t rows) { return (rows + kSubRows - 1) / kSubRows; }
+
+hipError_t launch_gemv_rows(const GemvParams &p, hipStream_t stream) {
+    using Kernel = void (*)(GemvParams);
+    static const Kernel kernels[4] = {gemv_rows_kernel<false, 1>, gemv_rows_kernel<false, 2>,
+                                      gemv_rows_kernel<true, 1>, gemv_rows_kernel<true, 2>};
+    if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || p.kb < kGemvRsWaves || p.nseg == 0 || p.nseg > 4)
+        return hipErrorInvalidValue;
+    const size_t lds = (size_t)kGemvRsWaves * gemv_rows_wave_lds(p.m);
+    hipLaunchKernelGGL(kernels[(p.x_vec ? 2 : 0) + (p.m > 4 ? 1 : 0)], dim3(p.nctas), dim3(kGemvRsThreads), lds,
+                       stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace q35mm

@@ -101,6 +101,21 @@ uint32_t gemv_norm_cols(uint32_t k);
 size_t gemv_norm_lds_bytes(uint32_t m, uint32_t norm_cols);
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 
+// Row-split decode GEMV (gemv_rows.hip): one workgroup per 32-row sub-tile,
+// kGemvRsWaves wavefronts splitting K, no partial outputs between
+// workgroups.  Used for the weights gemv_rows_shape() selects (by shape only,
+// so batch and multi-weight results stay those of single calls); activations
+// plain (kXPlain), optional residual.  Segments: cta_begin / nctas =
+// gemv_rows_ctas(rows); ws, cnt, max_range unused.
+constexpr uint32_t kGemvRsWaves = 4;
+constexpr uint32_t kGemvRsThreads = 64 * kGemvRsWaves;
+constexpr uint32_t kGemvRsMaxKb = 64;   // K blocks; longer K streams better with stream-K
+// Per wavefront: two A-operand slots of 256 * stage_rows(m) bytes + a zero slot.
+__host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 512 * stage_rows(m) + 16; }
+bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus);
+uint32_t gemv_rows_ctas(uint32_t rows);
+hipError_t launch_gemv_rows(const GemvParams &p, hipStream_t stream);
+
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
 constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64

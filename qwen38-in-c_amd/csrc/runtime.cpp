@@ -93,6 +93,7 @@ struct Device {
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
     bool mlp_unfused = false;   // Q35MM_MLP_UNFUSED=1: separate neighbour kernels on the GEMV path
+    bool gemv_rows = true;      // Q35MM_GEMV_ROWSPLIT=0: every weight on the stream-K GEMV
 };
 
 std::recursive_mutex g_mu;
@@ -118,6 +119,7 @@ int ensure_device() {
     g_dev.mlp_unfused = env_u32("Q35MM_MLP_UNFUSED", 0) != 0;
     g_dev.cus = (uint32_t)prop.multiProcessorCount;
     g_dev.gemv_per_cu = std::max(1u, env_u32("Q35MM_GEMV_CTAS_PER_CU", kGemvCtasPerCu));
+    g_dev.gemv_rows = env_u32("Q35MM_GEMV_ROWSPLIT", 1) != 0;
     return Q35MM_OK;
 }
 
@@ -268,6 +270,10 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 // cheaper.
 constexpr uint32_t kMlpFusedSwiGLUMaxM = 2;
 
+// Which decode GEMV a weight runs on; fixed by its shape (and the device),
+// never by m or by the other weights of a call.
+bool uses_gemv_rows(const Weight &w) { return g_dev.gemv_rows && gemv_rows_shape(w.rows, w.kb, g_dev.cus); }
+
 int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
                    float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid) {
     GemvParams p{};
@@ -285,6 +291,28 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     p.nseg = nseg;
     p.x_vec = (aligned16(dX) && cols % 8 == 0 && (!in.x2 || aligned16(in.x2)) &&
                (!in.norm_w || aligned16(in.norm_w))) ? 1u : 0u;
+    if (uses_gemv_rows(w[0]->w)) {
+        // the callers keep row-split weights on plain activations
+        if (in.xmode != kXPlain) return set_error(Q35MM_EINVAL, "row-split GEMV takes plain activations");
+        uint32_t cta = 0;
+        for (uint32_t s = 0; s < nseg; s++) {
+            const Weight &ws = w[s]->w;
+            GemvSeg &g = p.seg[s];
+            g.codes = ws.codes;
+            g.scale = ws.scale;
+            g.y = dY[s];
+            g.resid = resid ? resid[s] : nullptr;
+            g.rows = ws.rows;
+            g.ldy = ws.rows;
+            g.nb = ws.nb;
+            g.cta_begin = cta;
+            g.nctas = gemv_rows_ctas(ws.rows);
+            cta += g.nctas;
+        }
+        p.nctas = cta;
+        HIP_TRY(launch_gemv_rows(p, st));
+        return Q35MM_OK;
+    }
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &ws = w[s]->w;
@@ -320,21 +348,31 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     return Q35MM_OK;
 }
 
+// Weights sharing K, in groups of up to 8 tokens; stream-K weights share one
+// launch, row-split weights another.
 int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
              float *const *dY, hipStream_t st, const GemvInput &in = GemvInput(),
              float *const *resid = nullptr) {
     const uint32_t cols = w[0]->w.cols;
     for (uint32_t t0 = 0; t0 < m; t0 += kGemvMaxM) {
         const uint32_t mg = std::min(kGemvMaxM, m - t0);
-        float *ys[4], *rs[4];
-        for (uint32_t s = 0; s < nseg; s++) {
-            ys[s] = dY[s] + (size_t)t0 * w[s]->w.rows;
-            rs[s] = resid ? resid[s] + (size_t)t0 * w[s]->w.rows : nullptr;
-        }
         GemvInput ig = in;
         if (ig.x2) ig.x2 += (size_t)t0 * cols;
-        int rc = run_gemv_group(w, nseg, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr);
-        if (rc) return rc;
+        for (int rows_split = 0; rows_split < 2; rows_split++) {
+            const q35mm_weight *wg[4];
+            float *ys[4], *rs[4];
+            uint32_t n = 0;
+            for (uint32_t s = 0; s < nseg; s++) {
+                if (uses_gemv_rows(w[s]->w) != (rows_split != 0)) continue;
+                wg[n] = w[s];
+                ys[n] = dY[s] + (size_t)t0 * w[s]->w.rows;
+                rs[n] = resid ? resid[s] + (size_t)t0 * w[s]->w.rows : nullptr;
+                n++;
+            }
+            if (!n) continue;
+            int rc = run_gemv_group(wg, n, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr);
+            if (rc) return rc;
+        }
     }
     return Q35MM_OK;
 }
@@ -1027,9 +1065,12 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         // kMlpFusedSwiGLUMaxM tokens (every workgroup evaluates it for its
         // own K range), the residual add always in the down GEMV's epilogue.
         // Q35MM_MLP_UNFUSED=1 runs the separate kernels instead.
+        // A row-split weight takes plain activations: its neighbour runs as
+        // the separate kernel, which gives the same bits.
         const uint32_t mg = std::min(m, kGemvMaxM);
-        const bool fuse_norm = !g_dev.mlp_unfused && gemv_norm_fits(mg, H);
-        const bool fuse_swiglu = !g_dev.mlp_unfused && m <= kMlpFusedSwiGLUMaxM;
+        const bool fuse_norm = !g_dev.mlp_unfused && gemv_norm_fits(mg, H) && !uses_gemv_rows(gate->w) &&
+                               !uses_gemv_rows(up->w);
+        const bool fuse_swiglu = !g_dev.mlp_unfused && m <= kMlpFusedSwiGLUMaxM && !uses_gemv_rows(down->w);
         const q35mm_weight *gu[2] = {gate, up};
         float *gy[2] = {g, u};
         GemvInput norm;
