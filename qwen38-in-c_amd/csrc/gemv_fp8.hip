@@ -4,7 +4,8 @@
 // Replaces the hot loop of qwen35-c/src/q35_mm.c:88-198 (mm_fp8_row called
 // by q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4).
 //
-// Arithmetic.  Weights are converted e4m3 -> bf16 in registers (exact) and
+// Arithmetic.  Weights are converted e4m3 -> bf16 in registers (exact, two
+// codes per v_cvt_scalef32_pk_bf16_fp8 at scale 1.0) and
 // fed to v_mfma_f32_32x32x16_bf16.  Activations are fp32; each is split
 // exactly into three bf16 parts x = p0 + p1 + p2, and the A-operand rows are
 // m = t + 8p (token t < 8, part p < 3), so one MFMA forms the three partial
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
         for (int j = 0; j < 4; j++) {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
-                const bf16x8_t bop = e4m3x8_to_bf16x8(wq[j][2 * q], wq[j][2 * q + 1]);
+                const bf16x8_t bop = e4m3x8_to_bf16x8_cvt(wq[j][2 * q], wq[j][2 * q + 1], 1.0f);
                 const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
                 part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
             }

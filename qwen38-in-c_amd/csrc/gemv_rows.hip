@@ -39,32 +39,44 @@ namespace {
 
 constexpr uint32_t kRsDepth = 4;   // K blocks in flight per wavefront
 
-// The activations of one K block for all m tokens: 8-column vector
-// v < 16m (token v/16, block columns (v%16)*8 ..) is the (v/64)-th vector
-// of lane v%64.  Loads are unconditional (token and columns clamped), so the
-// waits before each block stay static; stage_xblock masks what is not real.
-template <uint32_t NV>
+// The activations of one K block for all m tokens.  MT = m rounded up to a
+// power of two (1, 2, 4, 8); lane l serves token l / (64/MT) and the
+// G = 2*MT block columns starting at (l % (64/MT)) * G, so every lane does
+// the same share of the split whatever m is.  Loads are unconditional
+// (token and columns clamped), so the waits before each block stay static;
+// stage_xblock masks what is not real.
+template <uint32_t MT>
 struct XBlock {
-    float v[NV][8];
+    static constexpr uint32_t kG = 2 * MT;          // columns per lane
+    static constexpr uint32_t kLanesPerToken = 64 / MT;
+    float v[kG];
 };
 
-template <bool VEC, uint32_t NV>
-__device__ __forceinline__ void load_xblock(XBlock<NV> &xb, const float *x, uint32_t ldx, uint32_t m, uint32_t k,
+template <bool VEC, uint32_t MT>
+__device__ __forceinline__ void load_xblock(XBlock<MT> &xb, const float *x, uint32_t ldx, uint32_t m, uint32_t k,
                                             uint32_t kb, uint32_t lane) {
-#pragma unroll
-    for (uint32_t u = 0; u < NV; u++) {
-        const uint32_t v = min(lane + 64 * u, 16 * m - 1);
-        const uint32_t kg = kb * kBlock + (v & 15) * 8;
-        const float *row = x + (size_t)(v >> 4) * ldx;
-        if constexpr (VEC) {   // rows 16-byte aligned, k % 8 == 0
-            const float4 *q = reinterpret_cast<const float4 *>(row + min(kg, k - 8));
-            const float4 a = q[0], b = q[1];
-            xb.v[u][0] = a.x; xb.v[u][1] = a.y; xb.v[u][2] = a.z; xb.v[u][3] = a.w;
-            xb.v[u][4] = b.x; xb.v[u][5] = b.y; xb.v[u][6] = b.z; xb.v[u][7] = b.w;
+    constexpr uint32_t G = XBlock<MT>::kG, L = XBlock<MT>::kLanesPerToken;
+    const uint32_t t = min(lane / L, m - 1);
+    const uint32_t kg = kb * kBlock + (lane % L) * G;
+    const float *row = x + (size_t)t * ldx;
+    if constexpr (VEC) {
+        // Rows 16-byte aligned and k % 8 == 0: every group of min(G, 4)
+        // columns is wholly inside or wholly past the row, so clamping each
+        // group on its own keeps the valid ones in place (a 16-column load
+        // clamped as one piece would shift them when k % 16 == 8).
+        if constexpr (G == 2) {
+            const float2 a = *reinterpret_cast<const float2 *>(row + min(kg, k - 2));
+            xb.v[0] = a.x; xb.v[1] = a.y;
         } else {
 #pragma unroll
-            for (uint32_t e = 0; e < 8; e++) xb.v[u][e] = row[min(kg + e, k - 1)];
+            for (uint32_t i = 0; i < G / 4; i++) {
+                const float4 a = *reinterpret_cast<const float4 *>(row + min(kg + 4 * i, k - 4));
+                xb.v[4 * i] = a.x; xb.v[4 * i + 1] = a.y; xb.v[4 * i + 2] = a.z; xb.v[4 * i + 3] = a.w;
+            }
         }
+    } else {
+#pragma unroll
+        for (uint32_t e = 0; e < G; e++) xb.v[e] = row[min(kg + e, k - 1)];
     }
 }
 
@@ -72,35 +84,45 @@ __device__ __forceinline__ void load_xblock(XBlock<NV> &xb, const float *x, uint
 //   byte offset(c, q, ai, h) = (((c*2 + q) * R + ai) * 2 + h) * 16
 // for chunk c < 4, MFMA q < 2, A row ai = part*m + token, h = lane/32 of
 // the reading lane; the 16 bytes hold block columns c*32 + 16h + 8q + 0..7.
-// Columns >= k are staged as zero.
-template <uint32_t NV>
-__device__ __forceinline__ void stage_xblock(const XBlock<NV> &xb, uint8_t *slot, uint32_t m, uint32_t R, uint32_t k,
+// A lane writes its G columns' share of those 16-byte units (4, 8, 16 or
+// 2x16 bytes per part).  Columns >= k are staged as zero.
+template <uint32_t MT>
+__device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot, uint32_t m, uint32_t R, uint32_t k,
                                              uint32_t kb, uint32_t lane) {
+    constexpr uint32_t G = XBlock<MT>::kG, L = XBlock<MT>::kLanesPerToken;
+    const uint32_t t = lane / L;
+    if (t >= m) return;
+    const uint32_t col0 = (lane % L) * G, kg = kb * kBlock + col0;
+    float xv[G];
 #pragma unroll
-    for (uint32_t u = 0; u < NV; u++) {
-        const uint32_t v = lane + 64 * u;
-        if (v < 16 * m) {
-            const uint32_t t = v >> 4, kk = (v & 15) * 8, kg = kb * kBlock + kk;
-            float xv[8];
+    for (uint32_t e = 0; e < G; e++) xv[e] = kg + e < k ? xb.v[e] : 0.0f;
+    uint32_t pr[3][G / 2];   // per part, packed bf16 pairs
 #pragma unroll
-            for (uint32_t e = 0; e < 8; e++) xv[e] = kg + e < k ? xb.v[u][e] : 0.0f;
-            uint32_t p0[4], p1[4], p2[4];
+    for (uint32_t e = 0; e < G / 2; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], pr[0][e], pr[1][e], pr[2][e]);
 #pragma unroll
-            for (uint32_t e = 0; e < 4; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], p0[e], p1[e], p2[e]);
-            const uint32_t c = kk >> 5, h = (kk >> 4) & 1, q = (kk >> 3) & 1;
-            const uint32_t base = (c * 2 + q) * R;
-            *reinterpret_cast<u32x4_t *>(slot + ((base + 0 * m + t) * 2 + h) * 16) = u32x4_t{p0[0], p0[1], p0[2], p0[3]};
-            *reinterpret_cast<u32x4_t *>(slot + ((base + 1 * m + t) * 2 + h) * 16) = u32x4_t{p1[0], p1[1], p1[2], p1[3]};
-            *reinterpret_cast<u32x4_t *>(slot + ((base + 2 * m + t) * 2 + h) * 16) = u32x4_t{p2[0], p2[1], p2[2], p2[3]};
+    for (uint32_t part = 0; part < 3; part++) {
+        const uint32_t ai = part * m + t;
+#pragma unroll
+        for (uint32_t u = 0; u < (G + 7) / 8; u++) {   // 8-column units covered by this lane
+            const uint32_t col = col0 + 8 * u;
+            const uint32_t c = col >> 5, h = (col >> 4) & 1, q = (col >> 3) & 1, e0 = col & 7;
+            uint8_t *dst = slot + (((c * 2 + q) * R + ai) * 2 + h) * 16 + e0 * 2;
+            if constexpr (G == 2) {
+                *reinterpret_cast<uint32_t *>(dst) = pr[part][0];
+            } else if constexpr (G == 4) {
+                *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pr[part][0], pr[part][1]};
+            } else {
+                *reinterpret_cast<u32x4_t *>(dst) =
+                    u32x4_t{pr[part][4 * u], pr[part][4 * u + 1], pr[part][4 * u + 2], pr[part][4 * u + 3]};
+            }
         }
     }
 }
 
 }  // namespace
 
-// NV = 8-column activation vectors per lane and K block: 1 for m <= 4,
-// 2 for m <= 8.
-template <bool VEC, uint32_t NV>
+// MT = m rounded up to a power of two.
+template <bool VEC, uint32_t MT>
 __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[kGemvRsWaves][kGemvMaxM][kSubRows];
@@ -136,21 +158,21 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     const float *scale = sg.scale + (size_t)g * KB;
     u32x4_t buf[kRsDepth][4];
     float scs[kRsDepth];
-    XBlock<NV> xr[kRsDepth];
+    XBlock<MT> xr[kRsDepth];
     auto load = [&](uint32_t d, uint32_t b) {
         const uint8_t *src = codes + (size_t)b * kBlockBytes;
 #pragma unroll
         for (uint32_t j = 0; j < 4; j++) buf[d][j] = *reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes);
         scs[d] = scale[b];
-        load_xblock<VEC, NV>(xr[d], p.x, p.ldx, M, p.k, min(b + 1, k1 - 1), lane);
+        load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, min(b + 1, k1 - 1), lane);
     };
-    XBlock<NV> x0;
-    load_xblock<VEC, NV>(x0, p.x, p.ldx, M, p.k, k0, lane);
+    XBlock<MT> x0;
+    load_xblock<VEC, MT>(x0, p.x, p.ldx, M, p.k, k0, lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (uint32_t d = 0; d + 1 < kRsDepth; d++) load(d, min(k0 + d, k1 - 1));
     __builtin_amdgcn_sched_barrier(0);
-    stage_xblock<NV>(x0, wbase, M, R, p.k, k0, lane);   // waits for x0 only: loads complete in order
+    stage_xblock<MT>(x0, wbase, M, R, p.k, k0, lane);   // waits for x0 only: loads complete in order
 
     f32x16_t acc = {};
     const f32x16_t zero = {};
@@ -167,20 +189,22 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
 #pragma unroll
                 for (uint32_t i = 0; i < 8; i++)
                     araw[i] = *reinterpret_cast<const u32x4_t *>(arow + par * a_slot + i * a_step);
-                if (bb + 1 < k1) stage_xblock<NV>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, bb + 1, lane);
+                if (bb + 1 < k1) stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, bb + 1, lane);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16_t part;
 #pragma unroll
                 for (uint32_t j = 0; j < 4; j++)
 #pragma unroll
                     for (uint32_t q = 0; q < 2; q++) {
-                        const bf16x8_t bop = e4m3x8_to_bf16x8(buf[d][j][2 * q], buf[d][j][2 * q + 1]);
+                        const bf16x8_t bop = e4m3x8_to_bf16x8_cvt(buf[d][j][2 * q], buf[d][j][2 * q + 1], 1.0f);
                         const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
                         part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
                     }
-                // rows 24..31 of the A operand carry nothing (regs 12..15)
+                // acc[r + 4p] holds part p of token 4h + (r & 3): only tokens
+                // below MT are scaled; rows 24..31 carry nothing (regs 12..15)
 #pragma unroll
-                for (uint32_t r = 0; r < 12; r++) acc[r] = __builtin_fmaf(scs[d], part[r], acc[r]);
+                for (uint32_t r = 0; r < 12; r++)
+                    if ((r & 3) < MT) acc[r] = __builtin_fmaf(scs[d], part[r], acc[r]);
             }
         }
     }
@@ -216,13 +240,15 @@ uint32_t gemv_rows_ctas(uint32_t rows) { return (rows + kSubRows - 1) / kSubRows
 
 hipError_t launch_gemv_rows(const GemvParams &p, hipStream_t stream) {
     using Kernel = void (*)(GemvParams);
-    static const Kernel kernels[4] = {gemv_rows_kernel<false, 1>, gemv_rows_kernel<false, 2>,
-                                      gemv_rows_kernel<true, 1>, gemv_rows_kernel<true, 2>};
+    static const Kernel kernels[8] = {gemv_rows_kernel<false, 1>, gemv_rows_kernel<false, 2>,
+                                      gemv_rows_kernel<false, 4>, gemv_rows_kernel<false, 8>,
+                                      gemv_rows_kernel<true, 1>,  gemv_rows_kernel<true, 2>,
+                                      gemv_rows_kernel<true, 4>,  gemv_rows_kernel<true, 8>};
     if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || p.kb < kGemvRsWaves || p.nseg == 0 || p.nseg > 4)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)kGemvRsWaves * gemv_rows_wave_lds(p.m);
-    hipLaunchKernelGGL(kernels[(p.x_vec ? 2 : 0) + (p.m > 4 ? 1 : 0)], dim3(p.nctas), dim3(kGemvRsThreads), lds,
-                       stream, p);
+    const uint32_t mt = p.m <= 1 ? 0 : p.m <= 2 ? 1 : p.m <= 4 ? 2 : 3;   // log2 of MT
+    hipLaunchKernelGGL(kernels[(p.x_vec ? 4 : 0) + mt], dim3(p.nctas), dim3(kGemvRsThreads), lds, stream, p);
     return hipGetLastError();
 }
 

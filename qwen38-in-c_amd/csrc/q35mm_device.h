@@ -47,35 +47,13 @@ __device__ __forceinline__ f32x2_t e4m3x2_to_f32(uint32_t w) {
     return __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
 }
 
-// Four e4m3 codes -> four bf16 packed in two dwords (element 0 in the low
-// half of the first dword).  Every finite e4m3 value has at most 4
-// significant bits and an exponent within bf16 range, so truncating the
-// exact fp32 to its top 16 bits is exact.
-__device__ __forceinline__ u32x2_t e4m3x4_to_bf16x4(uint32_t w) {
-    f32x2_t lo = e4m3x2_to_f32<false>(w);
-    f32x2_t hi = e4m3x2_to_f32<true>(w);
-    u32x2_t r;
-    // v_perm_b32: selector bytes 0-3 pick from the second source, 4-7 from
-    // the first; 0x07060302 keeps the upper halves of (src1, src0).
-    r.x = __builtin_amdgcn_perm(f32_bits(lo.y), f32_bits(lo.x), 0x07060302u);
-    r.y = __builtin_amdgcn_perm(f32_bits(hi.y), f32_bits(hi.x), 0x07060302u);
-    return r;
-}
-
-// Eight e4m3 codes (two dwords) -> bf16x8 MFMA operand.
-__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-    u32x2_t a = e4m3x4_to_bf16x4(w0);
-    u32x2_t b = e4m3x4_to_bf16x4(w1);
-    u32x4_t v = {a.x, a.y, b.x, b.y};
-    return __builtin_bit_cast(bf16x8_t, v);
-}
-
-// Eight e4m3 codes -> bf16x8 with gfx950's v_cvt_scalef32_pk_bf16_fp8 (two
-// codes per instruction; half the VALU of the path above).  The instruction
+// Eight e4m3 codes (two dwords) -> bf16x8 MFMA operand with gfx950's
+// v_cvt_scalef32_pk_bf16_fp8 (two codes per instruction).  The instruction
 // scales by 2^exponent(scale) only (E8M0 semantics: 1.5 acts as 1, 0 as
-// 2^-127).  With scale 1.0 every finite e4m3 value is exact in bf16, so the
-// result equals the one above (checked for all 256 codes); 0x7F / 0xFF give
-// NaN.
+// 2^-127).  Every finite e4m3 value has at most 4 significant bits and an
+// exponent within bf16 range, so at scale 1.0 the conversion is exact
+// (decode_bf16_kernel exposes it; checked for all 256 codes); 0x7F / 0xFF
+// give NaN.
 __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8_cvt(uint32_t w0, uint32_t w1, float pow2_scale) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, pow2_scale, false);

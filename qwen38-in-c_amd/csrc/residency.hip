@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void dequant_f32_kernel(const uint8_t *__restr
 }
 
 // out[r][c] = bf16 bits of e4m3(W[r][c]), unscaled: the operand conversion
-// of the GEMV and GEMM kernels (e4m3x8_to_bf16x8).
+// of the GEMV and GEMM kernels (e4m3x8_to_bf16x8_cvt at scale 1.0).
 __global__ __launch_bounds__(256) void decode_bf16_kernel(const uint8_t *__restrict__ tiled,
                                                           uint32_t rows, uint32_t cols,
                                                           uint32_t kb_total, uint32_t units,
@@ -92,8 +92,8 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const uint8_t *__restr
     const TileCoord c = unit_coord(u, kb_total);
     if (c.row >= rows || c.col >= cols) return;
     const u32x4_t q = *reinterpret_cast<const u32x4_t *>(tiled + (size_t)u * 16);
-    const bf16x8_t lo = e4m3x8_to_bf16x8(q[0], q[1]);
-    const bf16x8_t hi = e4m3x8_to_bf16x8(q[2], q[3]);
+    const bf16x8_t lo = e4m3x8_to_bf16x8_cvt(q[0], q[1], 1.0f);
+    const bf16x8_t hi = e4m3x8_to_bf16x8_cvt(q[2], q[3], 1.0f);
     const u32x4_t l4 = __builtin_bit_cast(u32x4_t, lo);
     const u32x4_t h4 = __builtin_bit_cast(u32x4_t, hi);
     uint16_t v[16];
