@@ -392,8 +392,8 @@ def main():
     n_launch = steps * 4
     roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("gemv_fp8_kernel_decode_m1_layer.md"),
-            "kernel": "gemv_fp8_kernel", "launches": n_launch,
+            "traffic": measured_traffic("decode_gemv_kernels_m1_layer.md"),
+            "kernel": "gemv_rows_kernel (qkv, o_proj, down) + gemv_fp8_kernel (gate+up)", "launches": n_launch,
             "avg_launch_us": round(el / n_launch * 1e6, 3),
             "bytes_per_launch": step_bytes[1] // 4}
     del g

@@ -3,7 +3,8 @@
 //
 // Replaces the same hot loop as gemv_fp8.hip (qwen35-c/src/q35_mm.c:88-198,
 // mm_fp8_row under q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4) for
-// the shapes gemv_rows_shape() selects, e.g. 5120->6144 and 4096->5120.
+// the shapes gemv_rows_shape() selects, e.g. 5120->6144, 4096->5120 and
+// 17408->5120.
 //
 // Decomposition.  One workgroup per 32-row sub-tile (the weight's
 // ceil(rows/32) sub-tiles fill between half and all of the CUs), and the

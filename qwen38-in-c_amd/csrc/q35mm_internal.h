@@ -109,7 +109,11 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 // gemv_rows_ctas(rows); ws, cnt, max_range unused.
 constexpr uint32_t kGemvRsWaves = 4;
 constexpr uint32_t kGemvRsThreads = 64 * kGemvRsWaves;
-constexpr uint32_t kGemvRsMaxKb = 64;   // K blocks; longer K streams better with stream-K
+// Every row-split workgroup splits all m*K activations itself, so that
+// redundant work grows with K*m: at 136 K blocks (17408 columns) row-split
+// still wins for m <= 4 and loses ~10% at m = 8; beyond 160 blocks
+// stream-K is kept.
+constexpr uint32_t kGemvRsMaxKb = 160;
 // Per wavefront: two A-operand slots of 256 * stage_rows(m) bytes + a zero slot.
 __host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 512 * stage_rows(m) + 16; }
 bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus);

@@ -1,11 +1,12 @@
 """Row-split decode GEMV (gemv_rows.hip) against the oracle, through the C ABI.
 
 On a 256-CU MI355X the row-split kernel takes the weights with 128..256
-32-row sub-tiles (4065..8192 rows) and 8..64 K blocks: the model's qkv
-(5120 -> 6144) and o_proj (4096 -> 5120), which the golden cases also cover.
+32-row sub-tiles (4065..8192 rows) and 8..160 K blocks: the model's qkv
+(5120 -> 6144), o_proj (4096 -> 5120) and down (17408 -> 5120), which the
+golden cases also cover.
 Here: ragged and maximal shapes of that class, unaligned activations (the
-scalar-load staging), every token count class (one or two activation
-vectors per lane), batch == n single calls and multi-weight == single calls
+scalar-load staging), every token count class (1, 2, 4 or 8 tokens per
+staging layout), batch == n single calls and multi-weight == single calls
 bit for bit -- also when one call mixes row-split and stream-K weights --
 and the MLP block when all three of its weights are row-split.
 
@@ -34,7 +35,8 @@ def _host(t):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1003, 4100), (4, 1003, 4100), (5, 1000, 4065), (8, 8192, 8192),
-                                   (3, 4096, 5120), (8, 5120, 6144), (2, 1024, 7777)])
+                                   (3, 4096, 5120), (8, 5120, 6144), (2, 1024, 7777), (6, 20480, 4100),
+                                   (7, 17400, 5000)])
 def test_row_split_shapes(q, oracle, wl, gpu, m, k, n):
     W, sc = wl.gen_weight_ragged(7 * n + k + m, n, k)
     X = wl.gen_act(n + m, m, k, outlier_frac=0.01)
