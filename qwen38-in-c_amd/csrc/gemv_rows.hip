@@ -153,18 +153,20 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     const uint32_t a_step = a_active ? R * 32 : 0;
     if (lane < 4) reinterpret_cast<uint32_t *>(wbase + 512 * R)[lane] = 0u;
 
-    // ---- ring: slot d holds the weights and scale of block b and the
-    // activations of block b+1 (clamped into the range) ----
+    // ---- block scales: lane i holds the scale of block k0 + i (a range has
+    // at most 64 blocks); v_readlane picks it per block, so no scalar load
+    // shares the LDS counter with the operand reads inside the loop ----
+    const float sc_lane = sg.scale[(size_t)g * KB + min(k0 + lane, k1 - 1)];
+
+    // ---- ring: slot d holds the weights of block b and the activations of
+    // block b+1 (clamped into the range) ----
     const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
-    const float *scale = sg.scale + (size_t)g * KB;
     u32x4_t buf[kRsDepth][4];
-    float scs[kRsDepth];
     XBlock<MT> xr[kRsDepth];
     auto load = [&](uint32_t d, uint32_t b) {
         const uint8_t *src = codes + (size_t)b * kBlockBytes;
 #pragma unroll
         for (uint32_t j = 0; j < 4; j++) buf[d][j] = *reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes);
-        scs[d] = scale[b];
         load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, min(b + 1, k1 - 1), lane);
     };
     XBlock<MT> x0;
@@ -175,6 +177,7 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     __builtin_amdgcn_sched_barrier(0);
     stage_xblock<MT>(x0, wbase, M, R, p.k, k0, lane);   // waits for x0 only: loads complete in order
 
+    // ---- stream ----
     f32x16_t acc = {};
     const f32x16_t zero = {};
     for (uint32_t b = k0; b < k1; b += kRsDepth) {
@@ -201,11 +204,13 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
                         const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
                         part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
                     }
+                const float sc =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), bb - k0));
                 // acc[r + 4p] holds part p of token 4h + (r & 3): only tokens
                 // below MT are scaled; rows 24..31 carry nothing (regs 12..15)
 #pragma unroll
                 for (uint32_t r = 0; r < 12; r++)
-                    if ((r & 3) < MT) acc[r] = __builtin_fmaf(scs[d], part[r], acc[r]);
+                    if ((r & 3) < MT) acc[r] = __builtin_fmaf(sc, part[r], acc[r]);
             }
         }
     }

@@ -114,6 +114,7 @@ constexpr uint32_t kGemvRsThreads = 64 * kGemvRsWaves;
 // still wins for m <= 4 and loses ~10% at m = 8; beyond 160 blocks
 // stream-K is kept.
 constexpr uint32_t kGemvRsMaxKb = 160;
+static_assert(kGemvRsMaxKb <= 64 * kGemvRsWaves, "a wavefront's block scales sit one per lane");
 // Per wavefront: two A-operand slots of 256 * stage_rows(m) bytes + a zero slot.
 __host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 512 * stage_rows(m) + 16; }
 bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus);
