@@ -139,7 +139,10 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t k0 = wv * KB / kGemvRsWaves, k1 = (wv + 1) * KB / kGemvRsWaves;   // KB >= waves
+    // K blocks of this wavefront: kbof(i) = k0 + i for i < n (KB >= waves).
+    // (Interleaving the wavefronts over K instead measured the same.)
+    const uint32_t k0 = wv * KB / kGemvRsWaves, n = (wv + 1) * KB / kGemvRsWaves - k0;
+    auto kbof = [&](uint32_t i) { return k0 + i; };
 
     // This wavefront's LDS: two A-operand slots and a 16-byte zero slot.
     // Lanes whose A row carries no token (t >= m, or rows 24..31) read the
@@ -153,47 +156,47 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     const uint32_t a_step = a_active ? R * 32 : 0;
     if (lane < 4) reinterpret_cast<uint32_t *>(wbase + 512 * R)[lane] = 0u;
 
-    // ---- block scales: lane i holds the scale of block k0 + i (a range has
+    // ---- block scales: lane i holds the scale of block kbof(i) (a range has
     // at most 64 blocks); v_readlane picks it per block, so no scalar load
     // shares the LDS counter with the operand reads inside the loop ----
-    const float sc_lane = sg.scale[(size_t)g * KB + min(k0 + lane, k1 - 1)];
+    const float sc_lane = sg.scale[(size_t)g * KB + kbof(min(lane, n - 1))];
 
     // ---- ring: slot d holds the weights of block b and the activations of
     // block b+1 (clamped into the range) ----
     const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
     u32x4_t buf[kRsDepth][4];
     XBlock<MT> xr[kRsDepth];
-    auto load = [&](uint32_t d, uint32_t b) {
-        const uint8_t *src = codes + (size_t)b * kBlockBytes;
+    auto load = [&](uint32_t d, uint32_t i) {
+        const uint8_t *src = codes + (size_t)kbof(i) * kBlockBytes;
 #pragma unroll
         for (uint32_t j = 0; j < 4; j++) buf[d][j] = *reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes);
-        load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, min(b + 1, k1 - 1), lane);
+        load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, kbof(min(i + 1, n - 1)), lane);
     };
     XBlock<MT> x0;
-    load_xblock<VEC, MT>(x0, p.x, p.ldx, M, p.k, k0, lane);
+    load_xblock<VEC, MT>(x0, p.x, p.ldx, M, p.k, kbof(0), lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (uint32_t d = 0; d + 1 < kRsDepth; d++) load(d, min(k0 + d, k1 - 1));
+    for (uint32_t d = 0; d + 1 < kRsDepth; d++) load(d, min(d, n - 1));
     __builtin_amdgcn_sched_barrier(0);
-    stage_xblock<MT>(x0, wbase, M, R, p.k, k0, lane);   // waits for x0 only: loads complete in order
+    stage_xblock<MT>(x0, wbase, M, R, p.k, kbof(0), lane);   // waits for x0 only: loads complete in order
 
     // ---- stream ----
     f32x16_t acc = {};
     const f32x16_t zero = {};
-    for (uint32_t b = k0; b < k1; b += kRsDepth) {
+    for (uint32_t b = 0; b < n; b += kRsDepth) {
 #pragma unroll
         for (uint32_t d = 0; d < kRsDepth; d++) {
             const uint32_t bb = b + d;
-            load((d + kRsDepth - 1) % kRsDepth, min(bb + kRsDepth - 1, k1 - 1));
+            load((d + kRsDepth - 1) % kRsDepth, min(bb + kRsDepth - 1, n - 1));
             // keep the scheduler from sinking these loads below block bb's math
             __builtin_amdgcn_sched_barrier(0);
-            if (bb < k1) {
-                const uint32_t par = (bb - k0) & 1;
+            if (bb < n) {
+                const uint32_t par = bb & 1;
                 u32x4_t araw[8];
 #pragma unroll
                 for (uint32_t i = 0; i < 8; i++)
                     araw[i] = *reinterpret_cast<const u32x4_t *>(arow + par * a_slot + i * a_step);
-                if (bb + 1 < k1) stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, bb + 1, lane);
+                if (bb + 1 < n) stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, kbof(bb + 1), lane);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16_t part;
 #pragma unroll
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
                         part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
                     }
                 const float sc =
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), bb - k0));
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), bb));
                 // acc[r + 4p] holds part p of token 4h + (r & 3): only tokens
                 // below MT are scaled; rows 24..31 carry nothing (regs 12..15)
 #pragma unroll
