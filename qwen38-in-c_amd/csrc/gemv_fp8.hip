@@ -269,17 +269,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
     // ---- weight stream: a ring of kGemvDepth blocks in registers ----
     // Loads are unconditional (block index clamped into the range; the few
     // repeated tail loads hit in cache) so that the wait before each block is
-    // a static vmcnt and kGemvDepth-1 blocks stay in flight.  Each block's
-    // scale travels with it through a matching ring.
+    // a static vmcnt and kGemvDepth-1 blocks stay in flight.  The range's
+    // block scales sit one per lane (lane i: block b0 + i) and v_readlane
+    // picks each, so no scalar load shares the LDS counter with the operand
+    // reads in the loop.
+    static_assert(kGemvMaxRangeBlocks <= 64, "a range's block scales sit one per lane");
     u32x4_t buf[kGemvDepth][4];
-    float scs[kGemvDepth];
+    float sc_lane = 0.0f;
     const uint8_t *codes = sg.codes + lane_off;
-    const float *scale = sg.scale;
-    auto load = [&](u32x4_t (&dst)[4], float &sc, uint32_t b) {
+    auto load = [&](u32x4_t (&dst)[4], uint32_t b) {
         const uint8_t *src = codes + (size_t)b * kBlockBytes;   // block b = g*KB + kb
 #pragma unroll
         for (int j = 0; j < 4; j++) dst[j] = ld16(src + j * kChunkBytes);
-        sc = scale[b];
     };
 
     // ---- prologue: activation loads, then the first weight blocks ----
@@ -292,8 +293,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
             stage_load<XM, VEC>(xpre[u], p, stage_item(min(threadIdx.x + u * kGemvThreads, nvec - 1), per_t, KB, b0));
     };
     auto ring_prologue = [&]() {
+        sc_lane = sg.scale[min(b0 + lane, b1 - 1)];
 #pragma unroll
-        for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], scs[d], min(b0 + d, b1 - 1));
+        for (uint32_t d = 0; d + 1 < kGemvDepth; d++) load(buf[d], min(b0 + d, b1 - 1));
     };
     if constexpr (XM == kXRmsNorm) {
         // x rows first, alone: their squares go to LDS (the stage takes it
@@ -434,7 +436,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
         for (uint32_t d = 0; d < kGemvDepth; d++) {
             const uint32_t bb = b + d;
             constexpr uint32_t nx = kGemvDepth - 1;
-            load(buf[(d + nx) % kGemvDepth], scs[(d + nx) % kGemvDepth], min(bb + nx, b1 - 1));
+            load(buf[(d + nx) % kGemvDepth], min(bb + nx, b1 - 1));
             // Keep the scheduler from sinking these loads below the math of
             // block bb (it would, to reuse their registers).
             __builtin_amdgcn_sched_barrier(0);
@@ -447,7 +449,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
                     gstart = bb;
                     acc = zero;
                 }
-                compute(buf[d], scs[d], bb - b0);
+                compute(buf[d], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), bb - b0)),
+                        bb - b0);
             }
         }
     }
