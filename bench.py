@@ -419,6 +419,7 @@ def main():
 
     # ---- MLP block at M = 1: RMSNorm -> gate/up -> SwiGLU -> down -> residual ----
     mlp_out = None
+    rows_split_off = os.environ.get("Q35MM_GEMV_ROWSPLIT", "1") == "0"   # the library's default: on
     if args.mlp:
         H, I = base[GATE][1], base[GATE][2]
         gen = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
@@ -446,10 +447,13 @@ def main():
                    "GBps": round(blk_bytes * steps / el_b / 1e9, 1),
                    "frac_of_hbm_peak": round(blk_bytes * steps / el_b / 1e9 / HBM_PEAK_GBS, 4),
                    "us_matmuls_only": round(el_m / steps * 1e6, 2),
-                   "launches_per_block": 2,
-                   "note": "q35mm_mlp at M=1: RMSNorm (exact eight-lane order) inside the gate+up GEMV, "
-                           "SwiGLU and the residual add inside the down GEMV; us_matmuls_only = the same "
-                           "two GEMV launches on ready activations"}
+                   "launches_per_block": 2 if rows_split_off else 3,
+                   "note": ("q35mm_mlp at M=1: RMSNorm (exact eight-lane order) inside the gate+up GEMV; "
+                            + ("SwiGLU and the residual add inside the down GEMV"
+                               if rows_split_off else
+                               "SwiGLU as its own kernel (down runs the row-split GEMV, which takes plain "
+                               "activations), the residual add inside the down GEMV")
+                            + "; us_matmuls_only = the gate+up and down GEMV launches on ready activations")}
         log(f"mlp block: {mlp_out}")
 
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----
