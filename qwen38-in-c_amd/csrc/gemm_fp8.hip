@@ -344,6 +344,152 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     }
 }
 
+// ---- the tail of a partial last round as 64x64 output tiles ----
+// When the tiles of the last round are few (at most one per 16 CUs), each
+// is cut into sixteen 64x64 output tiles, one workgroup per small tile.
+// Its eight wavefronts split K into contiguous K-block ranges and stream
+// their operands from memory straight into registers (nothing is shared
+// between wavefronts, so no LDS staging), each accumulating the whole 64x64
+// tile (2x2 MFMA tiles of 32x32) with the main kernel's arithmetic: bf16
+// operands, the accumulator kept in units of the last live block scale.
+// The eight partial tiles are added through LDS in wavefront order.  Against
+// K slices of whole 256x256 tiles this writes and re-reads no partial tiles
+// (64 MB for the 16 leftover tiles of a 512 x 34816 x 5120 product) and
+// needs no reduction kernel.
+constexpr uint32_t kTailTile = 64;
+constexpr uint32_t kTailPerTile = (kGemmTile / kTailTile) * (kGemmTile / kTailTile);   // 16
+constexpr uint32_t kTailDepth = 4;                                                      // chunks in flight
+constexpr uint32_t kTailLds = (kGemmThreads / 64) * kTailTile * kTailTile * 4;          // 128 KiB
+static_assert(kTailLds <= 160 * 1024, "LDS");
+
+__global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t tile = p.split_tile0 + blockIdx.x / kTailPerTile, st = blockIdx.x % kTailPerTile;
+    const uint32_t mt = tile % p.mtiles, nt = tile / p.mtiles;
+    const uint32_t row0 = mt * kGemmTile + (st & 3) * kTailTile;    // token rows
+    const uint32_t col0 = nt * kGemmTile + (st >> 2) * kTailTile;   // weight rows
+    if (row0 >= p.m || col0 >= p.nb * kBlock) return;               // the whole workgroup: no work
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t KB = p.kb;
+    const uint32_t nw = kGemmThreads / 64;
+    const uint32_t k0 = wv * KB / nw, k1 = (wv + 1) * KB / nw;        // empty when KB < nw
+    const uint32_t g = col0 / kBlock, s0 = (col0 % kBlock) / kSubRows; // weight group, first sub-tile
+    const uint32_t m32 = row0 / kSubRows;
+    const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb) + lane * 16;
+    const uint8_t *wb = p.codes + (size_t)g * KB * kBlockBytes + s0 * kSubBytes + lane * 16;
+    const float *sc_g = p.scale + (size_t)g * KB;
+
+    // Chunk c = 4 * (kb - k0) + j (32 columns): A for the two 32-row token
+    // sub-tiles and both MFMA halves, B (16 e4m3 codes per lane) for the
+    // two 32-row weight sub-tiles.
+    struct Chunk {
+        u32x4_t a[2][2];
+        u32x4_t b[2];
+    };
+    auto load = [&](Chunk &ch, uint32_t c) {
+        const uint32_t kb = k0 + c / 4, j = c % 4;
+#pragma unroll
+        for (uint32_t mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (uint32_t q = 0; q < 2; q++)
+                ch.a[mi][q] = *reinterpret_cast<const u32x4_t *>(
+                    xa + ((size_t)((m32 + mi) * KB + kb) * 8 + j * 2 + q) * kChunkBytes);
+#pragma unroll
+        for (uint32_t ni = 0; ni < 2; ni++)
+            ch.b[ni] = *reinterpret_cast<const u32x4_t *>(wb + (size_t)kb * kBlockBytes + ni * kSubBytes +
+                                                           j * kChunkBytes);
+    };
+
+    f32x16_t acc[2][2] = {};
+    float s_prev = 0.0f;   // units of the accumulator (0: nothing live yet)
+    if (k1 > k0) {
+        const uint32_t nc = (k1 - k0) * 4;
+        Chunk ring[kTailDepth];
+#pragma unroll
+        for (uint32_t d = 0; d + 1 < kTailDepth; d++) load(ring[d], min(d, nc - 1));
+        float keep = 1.0f;
+        float sc_next = sc_g[k0];
+        static_assert(kTailDepth == 4, "a K block starts at d == 0");
+        for (uint32_t c0 = 0; c0 < nc; c0 += kTailDepth) {
+#pragma unroll
+            for (uint32_t d = 0; d < kTailDepth; d++) {
+                const uint32_t c = c0 + d;
+                load(ring[(d + kTailDepth - 1) % kTailDepth], min(c + kTailDepth - 1, nc - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (c < nc) {
+                    if (d == 0) {
+                        // a new K block: bring the accumulator into its units
+                        // (block scale 0: the conversion scale 0 acts as
+                        // 2^-127, as in the main kernel)
+                        const uint32_t kb = k0 + c / 4;
+                        const float sc = sc_next;
+                        sc_next = sc_g[min(kb + 1, k1 - 1)];
+                        const bool live = sc != 0.0f;
+                        keep = live ? 1.0f : 0.0f;
+                        const float r = live ? (s_prev != 0.0f ? s_prev / sc : 0.0f) : 1.0f;
+#pragma unroll
+                        for (uint32_t mi = 0; mi < 2; mi++)
+#pragma unroll
+                            for (uint32_t ni = 0; ni < 2; ni++) acc[mi][ni] *= r;
+                        s_prev = live ? sc : s_prev;
+                    }
+                    const Chunk &ch = ring[d];
+#pragma unroll
+                    for (uint32_t q = 0; q < 2; q++) {
+                        bf16x8_t bw[2];
+#pragma unroll
+                        for (uint32_t ni = 0; ni < 2; ni++)
+                            bw[ni] = e4m3x8_to_bf16x8_cvt(ch.b[ni][2 * q], ch.b[ni][2 * q + 1], keep);
+#pragma unroll
+                        for (uint32_t mi = 0; mi < 2; mi++)
+#pragma unroll
+                            for (uint32_t ni = 0; ni < 2; ni++)
+                                acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8_t, ch.a[mi][q]), bw[ni],
+                                                           acc[mi][ni]);
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- partial tiles -> LDS (lane-major, 16 values per lane and MFMA
+    // tile), then added in wavefront order ----
+    float *red = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (uint32_t a = 0; a < 4; a++) {
+        f32x16_t v = acc[a >> 1][a & 1] * s_prev;
+#pragma unroll
+        for (uint32_t r4 = 0; r4 < 4; r4++)
+            *reinterpret_cast<float4 *>(red + ((wv * 4 + a) * 64 + lane) * 16 + 4 * r4) =
+                make_float4(v[4 * r4], v[4 * r4 + 1], v[4 * r4 + 2], v[4 * r4 + 3]);
+    }
+    __syncthreads();
+    // thread t: MFMA tile a = (t / 64) % 4, lane l = t % 64, values 8h..8h+7
+    const uint32_t l = threadIdx.x & 63, a = (threadIdx.x >> 6) & 3, h = threadIdx.x >> 8;
+    float sum[8];
+#pragma unroll
+    for (uint32_t w = 0; w < kGemmThreads / 64; w++) {
+        const float *src = red + ((w * 4 + a) * 64 + l) * 16 + 8 * h;
+        const float4 u0 = *reinterpret_cast<const float4 *>(src);
+        const float4 u1 = *reinterpret_cast<const float4 *>(src + 4);
+        const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (uint32_t e = 0; e < 8; e++) sum[e] = w == 0 ? v[e] : sum[e] + v[e];
+    }
+    const uint32_t mi = a >> 1, ni = a & 1;
+    const uint32_t col = col0 + ni * 32 + (l & 31);
+    if (col < p.rows) {
+#pragma unroll
+        for (uint32_t e = 0; e < 8; e++) {
+            const uint32_t r = 8 * h + e;
+            const uint32_t row = row0 + mi * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+            if (row < p.m) p.y[(size_t)row * p.ldy + col] = sum[e];
+        }
+    }
+}
+
 // Ordered sum of the K slices of split tiles: y = ((p_0 + p_1) + p_2) + ...
 // One thread per float4 of a partial tile (16384 per tile); the layout is
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
@@ -387,9 +533,10 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
 
 GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
     // Whole rounds of tiles run unsplit; the tiles of the last, partial round
-    // are cut along K so that round fills the device too.  A slice keeps at
-    // least two K blocks (four pipeline stages).  A K range longer than the
-    // LDS scale table (kGemmMaxSliceKb blocks) splits every tile.
+    // are cut so that round fills the device too: into 64x64 tiles when
+    // those fit one round (gemm_tail_kernel), else along K (a slice keeps at
+    // least two K blocks, four pipeline stages).  A K range longer than the
+    // LDS scale table (kGemmMaxSliceKb blocks) splits every tile along K.
     GemmPlan pl{};
     pl.mtiles = (m + kGemmTile - 1) / kGemmTile;
     pl.ntiles = (nb + 1) / 2;
@@ -402,6 +549,12 @@ GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
     }
     const uint32_t whole = tiles / cus * cus;
     const uint32_t rest = tiles - whole;
+    if (rest && rest * kTailPerTile <= cus) {
+        pl.split_tile0 = whole;
+        pl.nslices = 1;
+        pl.small_tail = 1;
+        return pl;
+    }
     const uint32_t s = rest ? std::min(cus / rest, std::max(1u, kb / 2)) : 1;
     pl.split_tile0 = s > 1 ? whole : tiles;
     pl.nslices = s > 1 ? s : 1;
@@ -419,10 +572,21 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTailLds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const uint32_t tiles = p.mtiles * p.ntiles;
+    if (p.small_tail) {
+        if (p.split_tile0)
+            hipLaunchKernelGGL(gemm_fp8_kernel, dim3(p.split_tile0), dim3(kGemmThreads), kGemmLds, stream, p);
+        if (p.split_tile0 < tiles)
+            hipLaunchKernelGGL(gemm_tail_kernel, dim3((tiles - p.split_tile0) * kTailPerTile), dim3(kGemmThreads),
+                               kTailLds, stream, p);
+        return hipGetLastError();
+    }
     const uint32_t grid = p.split_tile0 + (tiles - p.split_tile0) * p.nslices;
     hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
     if (p.split_tile0 < tiles) {

@@ -148,12 +148,14 @@ struct GemmParams {
     uint32_t ntiles;
     uint32_t split_tile0;
     uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
+    uint32_t small_tail; // 1: the tiles from split_tile0 on run as 64x64 tiles (gemm_tail_kernel)
 };
 
 struct GemmPlan {
-    uint32_t mtiles, ntiles, split_tile0, nslices;
-    uint32_t grid() const { return split_tile0 + (mtiles * ntiles - split_tile0) * nslices; }
-    size_t ws_bytes() const { return (size_t)(mtiles * ntiles - split_tile0) * nslices * kGemmTile * kGemmTile * 4; }
+    uint32_t mtiles, ntiles, split_tile0, nslices, small_tail;
+    size_t ws_bytes() const {
+        return small_tail ? 0 : (size_t)(mtiles * ntiles - split_tile0) * nslices * kGemmTile * kGemmTile * 4;
+    }
 };
 GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus);
 // X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
@@ -161,7 +163,8 @@ GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus);
 hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
                               uint32_t m32_tiles, uint32_t kb, uint16_t *xb,
                               hipStream_t stream);
-hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);   // + gemm_reduce when split
+// gemm_fp8_kernel, then gemm_reduce (K-split tail) or gemm_tail_kernel (64x64 tail)
+hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
 
 // ---- residency / conversions -----------------------------------------
 // Row-major raw codes (device) -> lane-order tiles (device).
