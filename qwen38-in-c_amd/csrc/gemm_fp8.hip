@@ -411,7 +411,6 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
         for (uint32_t d = 0; d + 1 < kTailDepth; d++) load(ring[d], min(d, nc - 1));
         float keep = 1.0f;
         float sc_next = sc_g[k0];
-        static_assert(kTailDepth == 4, "a K block starts at d == 0");
         for (uint32_t c0 = 0; c0 < nc; c0 += kTailDepth) {
 #pragma unroll
             for (uint32_t d = 0; d < kTailDepth; d++) {
@@ -419,7 +418,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
                 load(ring[(d + kTailDepth - 1) % kTailDepth], min(c + kTailDepth - 1, nc - 1));
                 __builtin_amdgcn_sched_barrier(0);
                 if (c < nc) {
-                    if (d == 0) {
+                    if ((c & 3) == 0) {
                         // a new K block: bring the accumulator into its units
                         // (block scale 0: the conversion scale 0 acts as
                         // 2^-127, as in the main kernel)

@@ -226,8 +226,13 @@ def test_gemm_full_prefill_shapes_sampled(q, oracle, wl, gpu, k, n):
     assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 256, 384), (100, 4700, 3000), (37, 4736, 3000), (129, 129, 129)])
+@pytest.mark.parametrize("m,k,n", [(64, 256, 384), (100, 4700, 3000), (37, 4736, 3000), (129, 129, 129),
+                                   (300, 1000, 700), (64, 17408, 64), (513, 640, 300)])
 def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
+    """Ragged m, k, n.  With at most one 256x256 tile per 16 CUs every tile
+    here runs as 64x64 tiles (gemm_tail_kernel): partial token and weight
+    rows, K not a multiple of 128, a K range longer than eight wavefronts'
+    share (17408), a third token tile holding one row (513)."""
     import torch
     W, sc = wl.gen_weight(m + k + n, n, k)
     X = wl.gen_act(m * k, m, k)
