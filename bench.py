@@ -8,8 +8,8 @@ five projections 5120->6144 (qkv), 4096->5120 (o_proj), 5120->17408 (gate),
 5120->17408 (up), 17408->5120 (down), called as the reference's decode
 calls them: gate and up share x and go through one q35_mm_fp8_multi4-style
 call (qwen35-c/src/q35_model.c:930-934), the others one call each -- four
-launches of the decode GEMV kernel, with weights and activations resident in
-HBM before timing starts.  Steps rotate over a pool of P distinct layer
+launches of the decode GEMV kernels, with weights and activations resident
+in HBM before timing starts.  Steps rotate over a pool of P distinct layer
 copies (default 8 x 320 MB = 2.56 GB) so the 256 MB Infinity Cache and the
 L2 cannot serve repeats.  The copies are one generated layer with per-row
 sign patterns flipped (code ^ 0x80 on a pseudo-random half of the rows), so
@@ -22,7 +22,11 @@ token (--stack-layers, 0 to skip), the BF16 lm_head matvec (q35_mm_bf16,
 (RMSNorm, gate+up, SwiGLU, down, residual add on device).
 
 value = algorithmic bytes of K steps / elapsed seconds (HIP events on the
-launch stream, launches replayed from a HIP graph), in GB/s.  Algorithmic
+launch stream, launches replayed from a HIP graph), in GB/s.  The timed
+region starts right after a device synchronize, and the first few hundred
+microseconds after one run slower (the device ramps back up), so the
+defaults time long regions: K = 256 steps (~18 ms) and 100 prefill calls
+per shape; 64 steps read ~3% lower, 10 prefill calls ~15% lower.  Algorithmic
 bytes per matmul = N*K (e4m3) + 4*ceil(N/128)*ceil(K/128) (fp32 scales) +
 4*M*K (x) + 4*M*N (y).
 
@@ -294,14 +298,14 @@ def bench_stragglers(q, wl, torch, dev, use_graph: bool, n: int = 512):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--pool", type=int, default=8)
     ap.add_argument("--eager", action="store_true", help="launch steps eagerly instead of from a HIP graph")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--prefill-reps", type=int, default=100)
     ap.add_argument("--no-blas", dest="blas", action="store_false",
                     help="skip the vendor bf16 GEMM (torch.mm -> hipBLASLt) timed beside the prefill GEMM")
     ap.add_argument("--no-mlp", dest="mlp", action="store_false",
