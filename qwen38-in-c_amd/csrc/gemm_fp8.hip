@@ -364,7 +364,7 @@ static_assert(kTailLds <= 160 * 1024, "LDS");
 
 __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t tile = p.split_tile0 + blockIdx.x / kTailPerTile, st = blockIdx.x % kTailPerTile;
+    const uint32_t tile = p.tail_tile0 + blockIdx.x / kTailPerTile, st = blockIdx.x % kTailPerTile;
     const uint32_t mt = tile % p.mtiles, nt = tile / p.mtiles;
     const uint32_t row0 = mt * kGemmTile + (st & 3) * kTailTile;    // token rows
     const uint32_t col0 = nt * kGemmTile + (st >> 2) * kTailTile;   // weight rows
@@ -532,14 +532,22 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
 
 GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
     // Whole rounds of tiles run unsplit; the tiles of the last, partial round
-    // are cut so that round fills the device too: into 64x64 tiles when
-    // those fit one round (gemm_tail_kernel), else along K (a slice keeps at
-    // least two K blocks, four pipeline stages).  A K range longer than the
-    // LDS scale table (kGemmMaxSliceKb blocks) splits every tile along K.
+    // are cut so that round fills the device too:
+    //  - into 64x64 tiles when those fit one round (gemm_tail_kernel);
+    //  - otherwise along K, as many slices as fill the CUs (a slice keeps at
+    //    least two K blocks, four pipeline stages).
+    // (Just over half a round -- 136 tiles of a 512 x 17408 x 5120 product
+    // -- runs one slice per tile: cutting half a round's tiles in two and the
+    // rest into 64x64 tiles took the main kernel from 110 to 80 us, but the
+    // slice reduction and the tail added 33 us.)
+    // A K range longer than the LDS scale table (kGemmMaxSliceKb blocks)
+    // splits every tile along K.
     GemmPlan pl{};
     pl.mtiles = (m + kGemmTile - 1) / kGemmTile;
     pl.ntiles = (nb + 1) / 2;
     const uint32_t tiles = pl.mtiles * pl.ntiles;
+    pl.tail_tile0 = tiles;
+    pl.nslices = 1;
     const uint32_t smin = (kb + kGemmMaxSliceKb - 1) / kGemmMaxSliceKb;
     if (smin > 1) {
         pl.split_tile0 = 0;
@@ -548,15 +556,17 @@ GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
     }
     const uint32_t whole = tiles / cus * cus;
     const uint32_t rest = tiles - whole;
-    if (rest && rest * kTailPerTile <= cus) {
-        pl.split_tile0 = whole;
-        pl.nslices = 1;
-        pl.small_tail = 1;
+    pl.split_tile0 = tiles;
+    if (!rest) return pl;
+    if (rest * kTailPerTile <= cus) {
+        pl.split_tile0 = pl.tail_tile0 = whole;
         return pl;
     }
-    const uint32_t s = rest ? std::min(cus / rest, std::max(1u, kb / 2)) : 1;
-    pl.split_tile0 = s > 1 ? whole : tiles;
-    pl.nslices = s > 1 ? s : 1;
+    const uint32_t s = std::min(cus / rest, std::max(1u, kb / 2));
+    if (s > 1) {
+        pl.split_tile0 = whole;
+        pl.nslices = s;
+    }
     return pl;
 }
 
@@ -578,20 +588,16 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
         attr_set = true;
     }
     const uint32_t tiles = p.mtiles * p.ntiles;
-    if (p.small_tail) {
-        if (p.split_tile0)
-            hipLaunchKernelGGL(gemm_fp8_kernel, dim3(p.split_tile0), dim3(kGemmThreads), kGemmLds, stream, p);
-        if (p.split_tile0 < tiles)
-            hipLaunchKernelGGL(gemm_tail_kernel, dim3((tiles - p.split_tile0) * kTailPerTile), dim3(kGemmThreads),
-                               kTailLds, stream, p);
-        return hipGetLastError();
-    }
-    const uint32_t grid = p.split_tile0 + (tiles - p.split_tile0) * p.nslices;
-    hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
-    if (p.split_tile0 < tiles) {
-        const uint32_t quads = (tiles - p.split_tile0) * (kGemmTile * kGemmTile / 4);
+    const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
+    const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
+    if (grid) hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
+    if (nsplit) {
+        const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3(quads / 256), dim3(256), 0, stream, p);
     }
+    if (p.tail_tile0 < tiles)
+        hipLaunchKernelGGL(gemm_tail_kernel, dim3((tiles - p.tail_tile0) * kTailPerTile), dim3(kGemmThreads),
+                           kTailLds, stream, p);
     return hipGetLastError();
 }
 

@@ -126,13 +126,15 @@ constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
 constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64
 constexpr uint32_t kGemmMaxSliceKb = 1024;  // K blocks one workgroup may cover
 
-// Work split.  Tiles (mt, nt) are numbered tile = nt * mtiles + mt.  Tiles
-// below split_tile0 are whole (one workgroup, written straight to y); the
-// rest are cut into nslices K slices each, whose partial tiles go to ws and
-// are added in slice order by gemm_reduce.  Workgroup b < split_tile0 owns
+// Work split.  Tiles (mt, nt) are numbered tile = nt * mtiles + mt, in three
+// consecutive ranges: tiles below split_tile0 are whole (one workgroup,
+// written straight to y); tiles in [split_tile0, tail_tile0) are cut into
+// nslices K slices each, whose partial tiles go to ws and are added in slice
+// order by gemm_reduce; tiles from tail_tile0 on run as sixteen 64x64 tiles
+// each (gemm_tail_kernel).  Workgroup b < split_tile0 of gemm_fp8_kernel owns
 // tile b; workgroup split_tile0 + u owns slice u % nslices of tile
-// split_tile0 + u / nslices.  With whole tiles first, the split workgroups
-// fill the CUs the last round of whole tiles leaves idle.
+// split_tile0 + u / nslices.  With whole tiles first, the split and tail
+// workgroups fill the CUs the last round of whole tiles leaves idle.
 struct GemmParams {
     const uint16_t *xb;  // lane-order bf16 activations, mtiles*256 rows
     const uint8_t *codes;
@@ -148,13 +150,13 @@ struct GemmParams {
     uint32_t ntiles;
     uint32_t split_tile0;
     uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
-    uint32_t small_tail; // 1: the tiles from split_tile0 on run as 64x64 tiles (gemm_tail_kernel)
+    uint32_t tail_tile0; // first tile of the 64x64 tail (= mtiles * ntiles: none)
 };
 
 struct GemmPlan {
-    uint32_t mtiles, ntiles, split_tile0, nslices, small_tail;
+    uint32_t mtiles, ntiles, split_tile0, nslices, tail_tile0;
     size_t ws_bytes() const {
-        return small_tail ? 0 : (size_t)(mtiles * ntiles - split_tile0) * nslices * kGemmTile * kGemmTile * 4;
+        return nslices > 1 ? (size_t)(tail_tile0 - split_tile0) * nslices * kGemmTile * kGemmTile * 4 : 0;
     }
 };
 GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus);

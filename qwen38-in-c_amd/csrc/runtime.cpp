@@ -412,7 +412,7 @@ int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hip
     p.ntiles = pl.ntiles;
     p.split_tile0 = pl.split_tile0;
     p.nslices = pl.nslices;
-    p.small_tail = pl.small_tail;
+    p.tail_tile0 = pl.tail_tile0;
     const uint32_t mtiles = pl.mtiles;
     HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles * (kGemmTile / kSubRows), w.kb, (uint16_t *)g_dev.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));

@@ -206,10 +206,11 @@ def test_gemm_golden_cases(q, oracle, wl, gpu, name):
     q.release(W)
 
 
-@pytest.mark.parametrize("k,n", [(5120, 34816), (17408, 5120)])
+@pytest.mark.parametrize("k,n", [(5120, 34816), (17408, 5120), (5120, 17408)])
 def test_gemm_full_prefill_shapes_sampled(q, oracle, wl, gpu, k, n):
     """Full M=512 prefill shapes on the GPU, checked on 384 sampled output
-    columns against the oracle."""
+    columns against the oracle: gate and up fused (256 whole tiles + a 64x64
+    tail), down (every tile in K slices), gate alone (136 whole tiles)."""
     import torch
     W, sc = wl.gen_weight(0x51E50002 + k, n, k)
     X = wl.gen_act(0x51E50102 + k, 512, k, bf16=True)
@@ -227,12 +228,13 @@ def test_gemm_full_prefill_shapes_sampled(q, oracle, wl, gpu, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 256, 384), (100, 4700, 3000), (37, 4736, 3000), (129, 129, 129),
-                                   (300, 1000, 700), (64, 17408, 64), (513, 640, 300)])
+                                   (300, 1000, 700), (64, 17408, 64), (513, 640, 300), (100, 512, 33000)])
 def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     """Ragged m, k, n.  With at most one 256x256 tile per 16 CUs every tile
     here runs as 64x64 tiles (gemm_tail_kernel): partial token and weight
     rows, K not a multiple of 128, a K range longer than eight wavefronts'
-    share (17408), a third token tile holding one row (513)."""
+    share (17408), a third token tile holding one row (513).  The last
+    shape has 129 whole tiles, the last holding 232 of its 256 rows."""
     import torch
     W, sc = wl.gen_weight(m + k + n, n, k)
     X = wl.gen_act(m * k, m, k)
