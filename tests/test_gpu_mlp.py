@@ -194,12 +194,14 @@ def test_mlp_block_real_shape(q, oracle, wl, gpu, m):
 
 
 @pytest.mark.parametrize("m,H,I", [(1, 640, 1664), (2, 640, 1664), (8, 5120, 1024), (13, 645, 1000),
-                                   (1, 8200, 256)])
+                                   (1, 8200, 256), (1, 5120, 17408)])
 def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
-    """The block entry point (on the decode path: RMSNorm fused into the
-    gate+up GEMV, SwiGLU and the residual add into the down GEMV) gives the
-    bits of the separate device calls it stands for (rmsnorm, gate+up,
-    swiglu, down, add)."""
+    """The block entry point gives the bits of the separate device calls it
+    stands for (rmsnorm, gate+up, swiglu, down, add), whichever fusion the
+    shapes select on the decode path: RMSNorm in the gate+up GEMV; SwiGLU in
+    a stream-K down GEMV's staging (m <= 2) or as its own kernel (row-split
+    down, as in the model's 5120 x 17408 block here, or m > 2); the residual
+    add in the down GEMV."""
     import torch
     _, dw = _mlp_weights(q, wl, H, I, wl.SEED_BASE + 0x320 + H)
     rng = np.random.default_rng(5)
