@@ -69,6 +69,24 @@ __device__ __forceinline__ void dma_1k(const uint8_t *g, lds_u8 *l) {
     __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
 }
 
+// The segment (weight) of a tile and the tile's position in it.  MULTI is a
+// compile-time choice: a single-weight launch indexes segment 0 statically,
+// which keeps the main kernel's registers as they are without segments.
+struct TileAt {
+    uint32_t seg, mt, nt;
+};
+template <bool MULTI>
+__device__ __forceinline__ TileAt tile_at(const GemmParams &p, uint32_t tile) {
+    uint32_t s = 0;
+    if constexpr (MULTI) {
+#pragma unroll
+        for (uint32_t i = 1; i < 4; i++)
+            if (i < p.nseg && tile >= p.seg[i].tile0) s = i;
+    }
+    const uint32_t lt = MULTI ? tile - p.seg[s].tile0 : tile;
+    return {s, lt % p.mtiles, lt / p.mtiles};
+}
+
 }  // namespace
 
 // X fp32 [m][ldx] -> bf16 (round to nearest even) in lane order.  Output
@@ -115,6 +133,7 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
     }
 }
 
+template <bool MULTI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     lds_u8 *const ring = (lds_u8 *)lds;
@@ -124,8 +143,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     const uint32_t u = split ? blockIdx.x - p.split_tile0 : 0;
     const uint32_t tile = split ? p.split_tile0 + u / S : blockIdx.x;
     const uint32_t sl = split ? u % S : 0;
-    const uint32_t mt = tile % p.mtiles;
-    const uint32_t nt = tile / p.mtiles;
+    const TileAt ta = tile_at<MULTI>(p, tile);
+    const GemmSeg &sg = p.seg[ta.seg];
+    const uint32_t mt = ta.mt, nt = ta.nt;
     const uint32_t KB = p.kb;
     const uint32_t kb0 = (sl * KB) / S, kb1 = ((sl + 1) * KB) / S;
     const uint32_t st0 = 2 * kb0, st1 = 2 * kb1;   // stages of 64 columns
@@ -155,7 +175,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     for (uint32_t i = 0; i < kBLoads; i++) {
         const uint32_t Q = wv * kBLoads + i;
         const uint32_t n32 = Q / 2;
-        const uint32_t nbk = min(nt * 2 + n32 / 4, p.nb - 1);
+        const uint32_t nbk = min(nt * 2 + n32 / 4, sg.nb - 1);
         boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
     }
     auto issue = [&](uint32_t st, uint32_t buf) {
@@ -167,7 +187,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
                    la + (wv * kALoads + i) * kChunkBytes);
 #pragma unroll
         for (uint32_t i = 0; i < kBLoads; i++)
-            dma_1k(p.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
+            dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
                    la + kStageA + (wv * kBLoads + i) * kChunkBytes);
     };
 
@@ -182,7 +202,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
         const uint32_t nbg = nt * 2 + g;
         float v = 0.0f;
-        if (nbg < p.nb && kk < kb1 - kb0) v = p.scale[(size_t)nbg * KB + kb0 + kk];
+        if (nbg < sg.nb && kk < kb1 - kb0) v = sg.scale[(size_t)nbg * KB + kb0 + kk];
         sc_lds[j] = v;
     }
     __syncthreads();
@@ -324,8 +344,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
                 for (uint32_t r = 0; r < 16; r++) {
                     const uint32_t mrow = mt * kGemmTile + out_row(i, r);
                     const uint32_t ncol = nt * kGemmTile + out_col(jn);
-                    if (mrow < p.m && ncol < p.rows)
-                        __builtin_nontemporal_store(acc[i][jn][r], p.y + (size_t)mrow * p.ldy + ncol);
+                    if (mrow < p.m && ncol < sg.rows)
+                        __builtin_nontemporal_store(acc[i][jn][r], sg.y + (size_t)mrow * sg.ldy + ncol);
                 }
         return;
     }
@@ -362,13 +382,15 @@ constexpr uint32_t kTailDepth = 4;                                              
 constexpr uint32_t kTailLds = (kGemmThreads / 64) * kTailTile * kTailTile * 4;          // 128 KiB
 static_assert(kTailLds <= 160 * 1024, "LDS");
 
+template <bool MULTI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t tile = p.tail_tile0 + blockIdx.x / kTailPerTile, st = blockIdx.x % kTailPerTile;
-    const uint32_t mt = tile % p.mtiles, nt = tile / p.mtiles;
-    const uint32_t row0 = mt * kGemmTile + (st & 3) * kTailTile;    // token rows
-    const uint32_t col0 = nt * kGemmTile + (st >> 2) * kTailTile;   // weight rows
-    if (row0 >= p.m || col0 >= p.nb * kBlock) return;               // the whole workgroup: no work
+    const TileAt ta = tile_at<MULTI>(p, tile);
+    const GemmSeg &sg = p.seg[ta.seg];
+    const uint32_t row0 = ta.mt * kGemmTile + (st & 3) * kTailTile;    // token rows
+    const uint32_t col0 = ta.nt * kGemmTile + (st >> 2) * kTailTile;   // weight rows
+    if (row0 >= p.m || col0 >= sg.nb * kBlock) return;                 // the whole workgroup: no work
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -378,8 +400,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     const uint32_t g = col0 / kBlock, s0 = (col0 % kBlock) / kSubRows; // weight group, first sub-tile
     const uint32_t m32 = row0 / kSubRows;
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb) + lane * 16;
-    const uint8_t *wb = p.codes + (size_t)g * KB * kBlockBytes + s0 * kSubBytes + lane * 16;
-    const float *sc_g = p.scale + (size_t)g * KB;
+    const uint8_t *wb = sg.codes + (size_t)g * KB * kBlockBytes + s0 * kSubBytes + lane * 16;
+    const float *sc_g = sg.scale + (size_t)g * KB;
 
     // Chunk c = 4 * (kb - k0) + j (32 columns): A for the two 32-row token
     // sub-tiles and both MFMA halves, B (16 e4m3 codes per lane) for the
@@ -479,12 +501,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     }
     const uint32_t mi = a >> 1, ni = a & 1;
     const uint32_t col = col0 + ni * 32 + (l & 31);
-    if (col < p.rows) {
+    if (col < sg.rows) {
 #pragma unroll
         for (uint32_t e = 0; e < 8; e++) {
             const uint32_t r = 8 * h + e;
             const uint32_t row = row0 + mi * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-            if (row < p.m) p.y[(size_t)row * p.ldy + col] = sum[e];
+            if (row < p.m) sg.y[(size_t)row * sg.ldy + col] = sum[e];
         }
     }
 }
@@ -493,6 +515,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
 // One thread per float4 of a partial tile (16384 per tile); the layout is
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
 // the partials are visible without any device-scope protocol.
+template <bool MULTI>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     constexpr uint32_t kTileQuads = kGemmTile * kGemmTile / 4;
     const uint32_t f = blockIdx.x * 256 + threadIdx.x;
@@ -519,18 +542,19 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const uint32_t t = fq % kGemmThreads, q = fq / kGemmThreads;
     const uint32_t lane = t & 63, wv = t >> 6, wm = wv & 1, wn = wv >> 1;
     const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
-    const uint32_t mt = tile % p.mtiles, nt = tile / p.mtiles;
-    const uint32_t row0 = mt * kGemmTile + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
-    const uint32_t col = nt * kGemmTile + wn * 64 + jn * 32 + (lane & 31);
+    const TileAt ta = tile_at<MULTI>(p, tile);
+    const GemmSeg &sg = p.seg[ta.seg];
+    const uint32_t row0 = ta.mt * kGemmTile + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+    const uint32_t col = ta.nt * kGemmTile + wn * 64 + jn * 32 + (lane & 31);
     const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
-    if (col < p.rows) {
+    if (col < sg.rows) {
 #pragma unroll
         for (uint32_t e = 0; e < 4; e++)
-            if (row0 + e < p.m) p.y[(size_t)(row0 + e) * p.ldy + col] = tv[e];
+            if (row0 + e < p.m) sg.y[(size_t)(row0 + e) * sg.ldy + col] = tv[e];
     }
 }
 
-GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
+GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus) {
     // Whole rounds of tiles run unsplit; the tiles of the last, partial round
     // are cut so that round fills the device too:
     //  - into 64x64 tiles when those fit one round (gemm_tail_kernel);
@@ -544,7 +568,7 @@ GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus) {
     // splits every tile along K.
     GemmPlan pl{};
     pl.mtiles = (m + kGemmTile - 1) / kGemmTile;
-    pl.ntiles = (nb + 1) / 2;
+    pl.ntiles = ntiles;
     const uint32_t tiles = pl.mtiles * pl.ntiles;
     pl.tail_tile0 = tiles;
     pl.nslices = 1;
@@ -576,13 +600,14 @@ hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
+template <bool MULTI>
+static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel<MULTI>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel),
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel<MULTI>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTailLds);
         if (e != hipSuccess) return e;
         attr_set = true;
@@ -590,15 +615,20 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     const uint32_t tiles = p.mtiles * p.ntiles;
     const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
     const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
-    if (grid) hipLaunchKernelGGL(gemm_fp8_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
+    if (grid) hipLaunchKernelGGL(gemm_fp8_kernel<MULTI>, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
     if (nsplit) {
         const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
-        hipLaunchKernelGGL(gemm_reduce_kernel, dim3(quads / 256), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(gemm_reduce_kernel<MULTI>, dim3(quads / 256), dim3(256), 0, stream, p);
     }
     if (p.tail_tile0 < tiles)
-        hipLaunchKernelGGL(gemm_tail_kernel, dim3((tiles - p.tail_tile0) * kTailPerTile), dim3(kGemmThreads),
+        hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3((tiles - p.tail_tile0) * kTailPerTile), dim3(kGemmThreads),
                            kTailLds, stream, p);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
+    if (p.nseg == 0 || p.nseg > 4) return hipErrorInvalidValue;
+    return p.nseg > 1 ? launch_gemm_t<true>(p, stream) : launch_gemm_t<false>(p, stream);
 }
 
 }  // namespace q35mm

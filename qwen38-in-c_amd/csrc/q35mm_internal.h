@@ -135,19 +135,28 @@ constexpr uint32_t kGemmMaxSliceKb = 1024;  // K blocks one workgroup may cover
 // tile b; workgroup split_tile0 + u owns slice u % nslices of tile
 // split_tile0 + u / nslices.  With whole tiles first, the split and tail
 // workgroups fill the CUs the last round of whole tiles leaves idle.
-struct GemmParams {
-    const uint16_t *xb;  // lane-order bf16 activations, mtiles*256 rows
+// One weight of a GEMM launch: several weights sharing K (the reference's
+// gate and up) run as one launch over the concatenation of their tiles;
+// segment s owns tiles [tile0, tile0 + mtiles * ((nb + 1) / 2)).
+struct GemmSeg {
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
-    float *ws;           // partial tiles of split tiles, 256 KiB each
-    uint32_t m;
     uint32_t rows;
     uint32_t ldy;
-    uint32_t kb;
     uint32_t nb;         // 128-row groups of the weight
+    uint32_t tile0;
+};
+
+struct GemmParams {
+    GemmSeg seg[4];
+    const uint16_t *xb;  // lane-order bf16 activations, mtiles*256 rows
+    float *ws;           // partial tiles of split tiles, 256 KiB each
+    uint32_t nseg;
+    uint32_t m;
+    uint32_t kb;
     uint32_t mtiles;
-    uint32_t ntiles;
+    uint32_t ntiles;     // 256-row weight tiles over all segments
     uint32_t split_tile0;
     uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
     uint32_t tail_tile0; // first tile of the 64x64 tail (= mtiles * ntiles: none)
@@ -159,7 +168,8 @@ struct GemmPlan {
         return nslices > 1 ? (size_t)(tail_tile0 - split_tile0) * nslices * kGemmTile * kGemmTile * 4 : 0;
     }
 };
-GemmPlan gemm_plan(uint32_t m, uint32_t nb, uint32_t kb, uint32_t cus);
+// ntiles: 256-row weight tiles of all segments together
+GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus);
 // X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
 // multiple of 32 (m32 tiles = rows_pad / 32).
 hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,

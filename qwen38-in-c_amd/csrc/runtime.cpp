@@ -385,12 +385,19 @@ bool gemm_fits(const Weight &w, uint32_t m) {
     return xb_bytes <= UINT32_MAX && w_bytes <= UINT32_MAX;
 }
 
-int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hipStream_t st) {
-    const Weight &w = wt->w;
-    if (!gemm_fits(w, m))
-        return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
-    const GemmPlan pl = gemm_plan(m, w.nb, w.kb, g_dev.cus);
-    const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
+// Weights sharing K (cols) and x, one launch over all their tiles.
+int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const float *dX, float *const *dY,
+             hipStream_t st) {
+    const Weight &w0 = wt[0]->w;
+    uint32_t ntiles = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        const Weight &w = wt[s]->w;
+        if (!gemm_fits(w, m))
+            return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
+        ntiles += (w.nb + 1) / 2;
+    }
+    const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus);
+    const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w0.kb * kBlock * sizeof(uint16_t);
     int rc = grow(g_dev.xb, xb_bytes, false);
     if (rc) return rc;
     if (pl.ws_bytes()) {
@@ -398,23 +405,31 @@ int run_gemm(const q35mm_weight *wt, uint32_t m, const float *dX, float *dY, hip
         if (rc) return rc;
     }
     GemmParams p{};
+    uint32_t tile0 = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        const Weight &w = wt[s]->w;
+        GemmSeg &g = p.seg[s];
+        g.codes = w.codes;
+        g.scale = w.scale;
+        g.y = dY[s];
+        g.rows = w.rows;
+        g.ldy = w.rows;
+        g.nb = w.nb;
+        g.tile0 = tile0;
+        tile0 += pl.mtiles * ((w.nb + 1) / 2);
+    }
+    p.nseg = nseg;
     p.xb = (const uint16_t *)g_dev.xb.ptr;
-    p.codes = w.codes;
-    p.scale = w.scale;
-    p.y = dY;
     p.ws = (float *)g_dev.ws.ptr;
     p.m = m;
-    p.rows = w.rows;
-    p.ldy = w.rows;
-    p.kb = w.kb;
-    p.nb = w.nb;
+    p.kb = w0.kb;
     p.mtiles = pl.mtiles;
     p.ntiles = pl.ntiles;
     p.split_tile0 = pl.split_tile0;
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
-    const uint32_t mtiles = pl.mtiles;
-    HIP_TRY(launch_act_to_bf16(dX, w.cols, m, w.cols, mtiles * (kGemmTile / kSubRows), w.kb, (uint16_t *)g_dev.xb.ptr, st));
+    HIP_TRY(launch_act_to_bf16(dX, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
+                               (uint16_t *)g_dev.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -426,9 +441,9 @@ int check_weight(const q35mm_weight *w) {
 
 int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hipStream_t st) {
     if (m == 0) return Q35MM_OK;
-    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(w->w, m)) return run_gemm(w, m, dX, dY, st);
     const q35mm_weight *ws[1] = {w};
     float *ys[1] = {dY};
+    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(w->w, m)) return run_gemm(ws, 1, m, dX, ys, st);
     return run_gemv(ws, 1, m, dX, ys, st);
 }
 
@@ -959,7 +974,9 @@ Q35MM_API int q35mm_gemm(const q35mm_weight *w, uint32_t m, const float *dX, flo
     if (rc) return rc;
     if (m == 0) return Q35MM_OK;
     if (!dX || !dY) return set_error(Q35MM_EINVAL, "null activation pointer");
-    return run_gemm(w, m, dX, dY, pick_stream(stream));
+    const q35mm_weight *ws[1] = {w};
+    float *ys[1] = {dY};
+    return run_gemm(ws, 1, m, dX, ys, pick_stream(stream));
 }
 
 Q35MM_API int q35mm_matmul_multi(const q35mm_weight *const *w, uint32_t nseg, uint32_t m,
@@ -977,13 +994,7 @@ Q35MM_API int q35mm_matmul_multi(const q35mm_weight *const *w, uint32_t nseg, ui
     hipStream_t st = pick_stream(stream);
     bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0;
     for (uint32_t s = 0; s < nseg && gemm; s++) gemm = gemm_fits(w[s]->w, m);
-    if (gemm) {
-        for (uint32_t s = 0; s < nseg; s++) {
-            rc = run_gemm(w[s], m, dX, dY[s], st);
-            if (rc) return rc;
-        }
-        return Q35MM_OK;
-    }
+    if (gemm) return run_gemm(w, nseg, m, dX, dY, st);   // one launch over all segments' tiles
     return run_gemv(w, nseg, m, dX, dY, st);
 }
 

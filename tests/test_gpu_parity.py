@@ -247,6 +247,27 @@ def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
 
 
+@pytest.mark.parametrize("m", [64, 300])
+def test_gemm_multi_segment(q, oracle, wl, gpu, m):
+    """q35mm_matmul_multi on the GEMM path: three weights sharing K run as one
+    launch over all their tiles (row counts 640, 3000 and 5000: odd row
+    groups, ragged last tiles).  Each output within the GEMM bars of the
+    oracle."""
+    import torch
+    k = 1000
+    Ws = [wl.gen_weight(95 + i, n, k) for i, n in enumerate((640, 3000, 5000))]
+    X = wl.gen_act(98, m, k)
+    ws = [q.Weight(*w) for w in Ws]
+    Ys = [torch.empty((m, w.rows), dtype=torch.float32, device=gpu) for w in ws]
+    q.matmul_multi(ws, _torch_dev(X, gpu), Ys)
+    torch.cuda.synchronize()
+    for (W, sc), Y in zip(Ws, Ys):
+        rel, mx = _gemm_check(Y.cpu().numpy(), oracle.mm_batch(W, sc, X))
+        assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (W.shape, rel, mx)
+    for w in ws:
+        w.free()
+
+
 def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
     """Blocks whose scale is 0 contribute nothing (the reference's
     lut[code] * 0): first K blocks of a row group, blocks in the middle and a
