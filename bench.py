@@ -473,7 +473,8 @@ def main():
         mlp_out["prefill_m512"] = {"us_per_block": round(el_p / reps_p * 1e6, 2),
                                    "TFLOPs": round(flops_p * reps_p / el_p / 1e12, 1),
                                    "note": "q35mm_mlp at 512 tokens: RMSNorm kernel, one GEMM launch over gate "
-                                           "and up, SwiGLU kernel, down GEMM, residual add kernel"}
+                                           "and up, the down GEMM forming SwiGLU while rounding its activations "
+                                           "to bf16 and adding the residual in its epilogue"}
         log(f"mlp block: {mlp_out}")
 
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----

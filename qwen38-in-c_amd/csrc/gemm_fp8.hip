@@ -94,8 +94,13 @@ __device__ __forceinline__ TileAt tile_at(const GemmParams &p, uint32_t tile) {
 //   row = m32*32 + lane%32, columns kb*128 + j*32 + (lane/32)*16 + q*8 + e.
 // One workgroup converts one 32-row x 128-column block: coalesced row reads
 // (512 B per row), a transpose through LDS, and 8 KiB of contiguous writes.
-// Rows >= m and columns >= k are zero.
-__global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restrict__ x, uint32_t ldx,
+// Rows >= m and columns >= k are zero.  With SWIGLU the converted value is
+// silu(x) * x2 (q35_kern_swiglu's arithmetic, swiglu1) of two inputs with the
+// same layout: the bits of swiglu_kernel followed by the plain conversion,
+// without writing and re-reading the fp32 product.
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ x2, uint32_t ldx,
                                                           uint32_t m, uint32_t k, uint32_t kb_total,
                                                           uint16_t *__restrict__ xb) {
     __shared__ __align__(16) uint16_t t[32][128 + 8];     // +8: spread rows over banks
@@ -108,14 +113,31 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
         const uint32_t row = m32 * 32 + r, col = kb * kBlock + c4 * 4;
         float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (row < m) {
-            const float *xp = x + (size_t)row * ldx + col;
-            if (col + 4 <= k && ((reinterpret_cast<uintptr_t>(xp) & 15) == 0)) {
-                const float4 f = *reinterpret_cast<const float4 *>(xp);
-                v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            const size_t o = (size_t)row * ldx + col;
+            const bool vec = col + 4 <= k && ((reinterpret_cast<uintptr_t>(x + o) & 15) == 0) &&
+                             (!SWIGLU || ((reinterpret_cast<uintptr_t>(x2 + o) & 15) == 0));
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (vec) {
+                const float4 f = *reinterpret_cast<const float4 *>(x + o);
+                a[0] = f.x; a[1] = f.y; a[2] = f.z; a[3] = f.w;
+                if constexpr (SWIGLU) {
+                    const float4 g = *reinterpret_cast<const float4 *>(x2 + o);
+                    b[0] = g.x; b[1] = g.y; b[2] = g.z; b[3] = g.w;
+                }
             } else {
 #pragma unroll
                 for (uint32_t e = 0; e < 4; e++)
-                    if (col + e < k) v[e] = xp[e];
+                    if (col + e < k) {
+                        a[e] = x[o + e];
+                        if constexpr (SWIGLU) b[e] = x2[o + e];
+                    }
+            }
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) {
+                if constexpr (SWIGLU)
+                    v[e] = col + e < k ? swiglu1(a[e], b[e]) : 0.0f;
+                else
+                    v[e] = a[e];
             }
         }
         u32x2_t w = {f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3])};
@@ -344,8 +366,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
                 for (uint32_t r = 0; r < 16; r++) {
                     const uint32_t mrow = mt * kGemmTile + out_row(i, r);
                     const uint32_t ncol = nt * kGemmTile + out_col(jn);
-                    if (mrow < p.m && ncol < sg.rows)
-                        __builtin_nontemporal_store(acc[i][jn][r], sg.y + (size_t)mrow * sg.ldy + ncol);
+                    if (mrow < p.m && ncol < sg.rows) {
+                        const size_t o = (size_t)mrow * sg.ldy + ncol;
+                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][r] : acc[i][jn][r],
+                                                    sg.y + o);
+                    }
                 }
         return;
     }
@@ -506,7 +531,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
         for (uint32_t e = 0; e < 8; e++) {
             const uint32_t r = 8 * h + e;
             const uint32_t row = row0 + mi * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-            if (row < p.m) sg.y[(size_t)row * sg.ldy + col] = sum[e];
+            if (row < p.m) {
+                const size_t o = (size_t)row * sg.ldy + col;
+                sg.y[o] = sg.resid ? sg.resid[o] + sum[e] : sum[e];
+            }
         }
     }
 }
@@ -550,7 +578,10 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     if (col < sg.rows) {
 #pragma unroll
         for (uint32_t e = 0; e < 4; e++)
-            if (row0 + e < p.m) sg.y[(size_t)(row0 + e) * sg.ldy + col] = tv[e];
+            if (row0 + e < p.m) {
+                const size_t o = (size_t)(row0 + e) * sg.ldy + col;
+                sg.y[o] = sg.resid ? sg.resid[o] + tv[e] : tv[e];
+            }
     }
 }
 
@@ -594,9 +625,14 @@ GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus) {
     return pl;
 }
 
-hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k, uint32_t m32_tiles,
-                              uint32_t kb, uint16_t *xb, hipStream_t stream) {
-    hipLaunchKernelGGL(act_to_bf16_kernel, dim3(m32_tiles * kb), dim3(256), 0, stream, x, ldx, m, k, kb, xb);
+hipError_t launch_act_to_bf16(const float *x, const float *x2, uint32_t ldx, uint32_t m, uint32_t k,
+                              uint32_t m32_tiles, uint32_t kb, uint16_t *xb, hipStream_t stream) {
+    if (x2)
+        hipLaunchKernelGGL(act_to_bf16_kernel<true>, dim3(m32_tiles * kb), dim3(256), 0, stream, x, x2, ldx, m, k,
+                           kb, xb);
+    else
+        hipLaunchKernelGGL(act_to_bf16_kernel<false>, dim3(m32_tiles * kb), dim3(256), 0, stream, x, x2, ldx, m, k,
+                           kb, xb);
     return hipGetLastError();
 }
 

@@ -142,6 +142,7 @@ struct GemmSeg {
     const uint8_t *codes;
     const float *scale;
     float *y;            // token-major [m][ldy]
+    const float *resid;  // optional [m][ldy]: y = resid + product (may equal y)
     uint32_t rows;
     uint32_t ldy;
     uint32_t nb;         // 128-row groups of the weight
@@ -171,10 +172,9 @@ struct GemmPlan {
 // ntiles: 256-row weight tiles of all segments together
 GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus);
 // X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
-// multiple of 32 (m32 tiles = rows_pad / 32).
-hipError_t launch_act_to_bf16(const float *x, uint32_t ldx, uint32_t m, uint32_t k,
-                              uint32_t m32_tiles, uint32_t kb, uint16_t *xb,
-                              hipStream_t stream);
+// multiple of 32 (m32 tiles = rows_pad / 32).  With x2: silu(x) * x2 first.
+hipError_t launch_act_to_bf16(const float *x, const float *x2, uint32_t ldx, uint32_t m, uint32_t k,
+                              uint32_t m32_tiles, uint32_t kb, uint16_t *xb, hipStream_t stream);
 // gemm_fp8_kernel, then gemm_reduce (K-split tail) or gemm_tail_kernel (64x64 tail)
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
 

@@ -385,9 +385,11 @@ bool gemm_fits(const Weight &w, uint32_t m) {
     return xb_bytes <= UINT32_MAX && w_bytes <= UINT32_MAX;
 }
 
-// Weights sharing K (cols) and x, one launch over all their tiles.
+// Weights sharing K (cols) and x, one launch over all their tiles.  Optional:
+// resid[s] (y = resid + product, may alias y) and x2 (the activations are
+// silu(x) * x2, formed while rounding them to bf16).
 int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const float *dX, float *const *dY,
-             hipStream_t st) {
+             hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr) {
     const Weight &w0 = wt[0]->w;
     uint32_t ntiles = 0;
     for (uint32_t s = 0; s < nseg; s++) {
@@ -412,6 +414,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         g.codes = w.codes;
         g.scale = w.scale;
         g.y = dY[s];
+        g.resid = resid ? resid[s] : nullptr;
         g.rows = w.rows;
         g.ldy = w.rows;
         g.nb = w.nb;
@@ -428,7 +431,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.split_tile0 = pl.split_tile0;
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
-    HIP_TRY(launch_act_to_bf16(dX, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
+    HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
                                (uint16_t *)g_dev.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
@@ -1111,16 +1114,18 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         HIP_TRY(launch_add_inplace(dX, y, nh, st));
         return Q35MM_OK;
     }
+    // Prefill: RMSNorm kernel; gate and up as one GEMM launch; the down GEMM
+    // forms silu(gate) * up while rounding its activations to bf16 and adds
+    // the residual in its epilogue (the bits of the separate calls).
     HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
     const q35mm_weight *gu[2] = {gate, up};
     float *gy[2] = {g, u};
-    rc = q35mm_matmul_multi(gu, 2, m, xn, gy, stream);
+    rc = run_gemm(gu, 2, m, xn, gy, st);
     if (rc) return rc;
-    HIP_TRY(launch_swiglu(g, u, g, ni, st));
-    rc = run_matmul(down, m, g, y, st);
-    if (rc) return rc;
-    HIP_TRY(launch_add_inplace(dX, y, nh, st));
-    return Q35MM_OK;
+    const q35mm_weight *dn[1] = {down};
+    float *dy[1] = {dX};
+    const float *res[1] = {dX};
+    return run_gemm(dn, 1, m, g, dy, st, res, u);
 }
 
 Q35MM_API int q35mm_quantize_f32(const float *dW, uint32_t rows, uint32_t cols, uint8_t *dCodes,
