@@ -394,10 +394,12 @@ def main():
             assert torch.equal(a, b), "graph replay differs from eager launch"
     log(f"M=1: {value:.1f} GB/s, {ms_per_step * 1e3:.1f} us/step ({'graph' if g is not None else 'eager'})")
     n_launch = steps * 4
+    rows_split_off = os.environ.get("Q35MM_GEMV_ROWSPLIT", "1") == "0"   # the library's default: on
     roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("decode_gemv_kernels_m1_layer.md"),
-            "kernel": "gemv_rows_kernel (qkv, o_proj, down) + gemv_fp8_kernel (gate+up)", "launches": n_launch,
+            "kernel": ("gemv_fp8_kernel (stream-K)" if rows_split_off else
+                       "gemv_rows_kernel (qkv, o_proj, gate+up, down)"), "launches": n_launch,
             "avg_launch_us": round(el / n_launch * 1e6, 3),
             "bytes_per_launch": step_bytes[1] // 4}
     del g
@@ -423,7 +425,6 @@ def main():
 
     # ---- MLP block at M = 1: RMSNorm -> gate/up -> SwiGLU -> down -> residual ----
     mlp_out = None
-    rows_split_off = os.environ.get("Q35MM_GEMV_ROWSPLIT", "1") == "0"   # the library's default: on
     if args.mlp:
         H, I = base[GATE][1], base[GATE][2]
         gen = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
@@ -451,12 +452,13 @@ def main():
                    "GBps": round(blk_bytes * steps / el_b / 1e9, 1),
                    "frac_of_hbm_peak": round(blk_bytes * steps / el_b / 1e9 / HBM_PEAK_GBS, 4),
                    "us_matmuls_only": round(el_m / steps * 1e6, 2),
-                   "launches_per_block": 2 if rows_split_off else 3,
-                   "note": ("q35mm_mlp at M=1: RMSNorm (exact eight-lane order) inside the gate+up GEMV; "
-                            + ("SwiGLU and the residual add inside the down GEMV"
+                   "launches_per_block": 2 if rows_split_off else 4,
+                   "note": ("q35mm_mlp at M=1: "
+                            + ("RMSNorm (exact eight-lane order) inside the gate+up GEMV; SwiGLU and the residual "
+                               "add inside the down GEMV"
                                if rows_split_off else
-                               "SwiGLU as its own kernel (down runs the row-split GEMV, which takes plain "
-                               "activations), the residual add inside the down GEMV")
+                               "RMSNorm and SwiGLU as their own kernels (gate, up and down run the row-split "
+                               "GEMV, which takes plain activations), the residual add inside the down GEMV")
                             + "; us_matmuls_only = the gate+up and down GEMV launches on ready activations")}
         # the same block on the prefill path: 512 tokens, gate and up as one
         # GEMM launch over both weights, SwiGLU and the residual add as kernels

@@ -1,13 +1,13 @@
 // gemv_rows.hip -- decode GEMV, m <= 8 tokens, row-split decomposition for
-// weights of a few thousand rows and a short K.
+// weights of at least a few thousand rows and a moderate K.
 //
 // Replaces the same hot loop as gemv_fp8.hip (qwen35-c/src/q35_mm.c:88-198,
 // mm_fp8_row under q35_mm_fp8 / q35_mm_fp8_batch / q35_mm_fp8_multi4) for
-// the shapes gemv_rows_shape() selects, e.g. 5120->6144, 4096->5120 and
-// 17408->5120.
+// the shapes gemv_rows_shape() selects, e.g. 5120->6144, 4096->5120,
+// 5120->17408 and 17408->5120.
 //
 // Decomposition.  One workgroup per 32-row sub-tile (the weight's
-// ceil(rows/32) sub-tiles fill between half and all of the CUs), and the
+// ceil(rows/32) sub-tiles fill at least half of the CUs), and the
 // workgroup's kGemvRsWaves wavefronts split K into contiguous ranges of K
 // blocks.  Each wavefront streams its range of the sub-tile (4 KiB per K
 // block, one 16-byte load per lane per 1 KiB chunk) through a ring of
@@ -242,7 +242,9 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
 
 bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus) {
     const uint32_t nsub = (rows + kSubRows - 1) / kSubRows;
-    return 2 * nsub >= cus && nsub <= cus && kb >= 2 * kGemvRsWaves && kb <= kGemvRsMaxKb;
+    // No upper bound on rows: a launch of several rounds of workgroups
+    // (5120 -> 2 x 17408: 1088 workgroups) still beats stream-K at m = 1.
+    return 2 * nsub >= cus && kb >= 2 * kGemvRsWaves && kb <= kGemvRsMaxKb;
 }
 
 uint32_t gemv_rows_ctas(uint32_t rows) { return (rows + kSubRows - 1) / kSubRows; }

@@ -1,9 +1,10 @@
 """Row-split decode GEMV (gemv_rows.hip) against the oracle, through the C ABI.
 
-On a 256-CU MI355X the row-split kernel takes the weights with 128..256
-32-row sub-tiles (4065..8192 rows) and 8..160 K blocks: the model's qkv
-(5120 -> 6144), o_proj (4096 -> 5120) and down (17408 -> 5120), which the
-golden cases also cover.
+On a 256-CU MI355X the row-split kernel takes the weights with at least
+128 32-row sub-tiles (4065 rows) and 8..160 K blocks: the model's qkv
+(5120 -> 6144), o_proj (4096 -> 5120), gate and up (5120 -> 17408) and down
+(17408 -> 5120), which the golden cases also cover.  Above 256 sub-tiles a
+launch runs several rounds of workgroups.
 Here: ragged and maximal shapes of that class, unaligned activations (the
 scalar-load staging), every token count class (1, 2, 4 or 8 tokens per
 staging layout), batch == n single calls and multi-weight == single calls
@@ -36,7 +37,7 @@ def _host(t):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1003, 4100), (4, 1003, 4100), (5, 1000, 4065), (8, 8192, 8192),
                                    (3, 4096, 5120), (8, 5120, 6144), (2, 1024, 7777), (6, 20480, 4100),
-                                   (7, 17400, 5000)])
+                                   (7, 17400, 5000), (1, 1024, 20000), (3, 2048, 9001)])
 def test_row_split_shapes(q, oracle, wl, gpu, m, k, n):
     W, sc = wl.gen_weight_ragged(7 * n + k + m, n, k)
     X = wl.gen_act(n + m, m, k, outlier_frac=0.01)
@@ -119,14 +120,15 @@ def test_mixed_matmul_multi_device_api(q, oracle, wl, gpu):
         w.free()
 
 
-@pytest.mark.parametrize("m", [1, 3])
-def test_mlp_block_all_row_split(q, oracle, wl, gpu, m):
-    """H = 4096, I = 8192: gate, up (8192 x 4096) and down (4096 x 8192) are
-    all row-split, so RMSNorm and SwiGLU run as their own kernels and the
+@pytest.mark.parametrize("m,H,I", [(1, 4096, 8192), (2, 4096, 8192), (3, 4096, 8192), (8, 1024, 4096),
+                                   (5, 1536, 4100)])
+def test_mlp_block_all_row_split(q, oracle, wl, gpu, m, H, I):
+    """Gate and up row-split (I >= 4065 rows, 8+ K blocks), so the RMSNorm
+    runs as its own kernel.  Down is row-split at H = 4096 (SwiGLU as its
+    own kernel too) and stream-K at H <= 1536 (SwiGLU in its staging); the
     residual add stays in the down GEMV.  Checked against the oracle's block
     and, bit for bit, against the separate calls."""
     import torch
-    H, I = 4096, 8192
     W = {nm: wl.gen_weight(0x400 + i, *((H, I) if nm == "down" else (I, H)))
          for i, nm in enumerate(("gate", "up", "down"))}
     dw = {nm: q.Weight(*v) for nm, v in W.items()}
