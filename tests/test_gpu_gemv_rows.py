@@ -121,11 +121,12 @@ def test_mixed_matmul_multi_device_api(q, oracle, wl, gpu):
 
 
 @pytest.mark.parametrize("m,H,I", [(1, 4096, 8192), (2, 4096, 8192), (3, 4096, 8192), (8, 1024, 4096),
-                                   (5, 1536, 4100)])
+                                   (5, 1536, 4100), (13, 1024, 4096)])
 def test_mlp_block_all_row_split(q, oracle, wl, gpu, m, H, I):
-    """Gate and up row-split (I >= 4065 rows, 8+ K blocks), so the RMSNorm
-    runs as its own kernel.  Down is row-split at H = 4096 (SwiGLU as its
-    own kernel too) and stream-K at H <= 1536 (SwiGLU in its staging); the
+    """Gate and up row-split (I >= 4065 rows, 8+ K blocks; ragged rows at
+    I = 4100, two token groups at m = 13), so the RMSNorm runs as its own
+    kernel.  Down is row-split at H = 4096 (SwiGLU as its own kernel too)
+    and stream-K at H <= 1536 (SwiGLU in its staging for m <= 2); the
     residual add stays in the down GEMV.  Checked against the oracle's block
     and, bit for bit, against the separate calls."""
     import torch
