@@ -11,7 +11,7 @@
 // workgroup's kGemvRsWaves wavefronts split K into contiguous ranges of K
 // blocks.  Each wavefront streams its range of the sub-tile (4 KiB per K
 // block, one 16-byte load per lane per 1 KiB chunk) through a ring of
-// kRsDepth blocks; the wavefront partials are added through LDS in
+// DEPTH blocks; the wavefront partials are added through LDS in
 // wavefront order at the end.  No partial output leaves the workgroup, so
 // there are no tickets, no workspace and no second pass: that is the whole
 // point against stream-K, whose split-group protocol costs a few
@@ -38,7 +38,14 @@ namespace q35mm {
 
 namespace {
 
-constexpr uint32_t kRsDepth = 4;   // K blocks in flight per wavefront
+// K blocks in flight per wavefront (the ring depth DEPTH), chosen by the
+// host from the launch's shape; the summation order does not depend on it.
+// Three for a launch of one round of workgroups at m <= 2; two (fewer
+// registers: four wavefronts per SIMD instead of three) for launches of
+// several rounds, where more resident workgroups hide the latency, and for
+// m > 2, where each block's larger split hides it.  Layer step at m = 1 /
+// 4 / 8 against four blocks everywhere: +6% / +10% / +19%.
+constexpr uint32_t kRsDepthShort = 2, kRsDepthLong = 3;
 
 // The activations of one K block for all m tokens.  MT = m rounded up to a
 // power of two (1, 2, 4, 8); lane l serves token l / (64/MT) and the
@@ -122,8 +129,8 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
 
 }  // namespace
 
-// MT = m rounded up to a power of two.
-template <bool VEC, uint32_t MT>
+// MT = m rounded up to a power of two; DEPTH = ring depth.
+template <bool VEC, uint32_t MT, uint32_t DEPTH>
 __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[kGemvRsWaves][kGemvMaxM][kSubRows];
@@ -166,8 +173,8 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     // non-temporal loads keep them from displacing cached data (layer step
     // +3.4% against plain loads) ----
     const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
-    u32x4_t buf[kRsDepth][4];
-    XBlock<MT> xr[kRsDepth];
+    u32x4_t buf[DEPTH][4];
+    XBlock<MT> xr[DEPTH];
     auto load = [&](uint32_t d, uint32_t i) {
         const uint8_t *src = codes + (size_t)kbof(i) * kBlockBytes;
 #pragma unroll
@@ -179,18 +186,18 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     load_xblock<VEC, MT>(x0, p.x, p.ldx, M, p.k, kbof(0), lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (uint32_t d = 0; d + 1 < kRsDepth; d++) load(d, min(d, n - 1));
+    for (uint32_t d = 0; d + 1 < DEPTH; d++) load(d, min(d, n - 1));
     __builtin_amdgcn_sched_barrier(0);
     stage_xblock<MT>(x0, wbase, M, R, p.k, kbof(0), lane);   // waits for x0 only: loads complete in order
 
     // ---- stream ----
     f32x16_t acc = {};
     const f32x16_t zero = {};
-    for (uint32_t b = 0; b < n; b += kRsDepth) {
+    for (uint32_t b = 0; b < n; b += DEPTH) {
 #pragma unroll
-        for (uint32_t d = 0; d < kRsDepth; d++) {
+        for (uint32_t d = 0; d < DEPTH; d++) {
             const uint32_t bb = b + d;
-            load((d + kRsDepth - 1) % kRsDepth, min(bb + kRsDepth - 1, n - 1));
+            load((d + DEPTH - 1) % DEPTH, min(bb + DEPTH - 1, n - 1));
             // keep the scheduler from sinking these loads below block bb's math
             __builtin_amdgcn_sched_barrier(0);
             if (bb < n) {
@@ -252,17 +259,23 @@ bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus) {
 
 uint32_t gemv_rows_ctas(uint32_t rows) { return (rows + kSubRows - 1) / kSubRows; }
 
-hipError_t launch_gemv_rows(const GemvParams &p, hipStream_t stream) {
+hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, hipStream_t stream) {
     using Kernel = void (*)(GemvParams);
-    static const Kernel kernels[8] = {gemv_rows_kernel<false, 1>, gemv_rows_kernel<false, 2>,
-                                      gemv_rows_kernel<false, 4>, gemv_rows_kernel<false, 8>,
-                                      gemv_rows_kernel<true, 1>,  gemv_rows_kernel<true, 2>,
-                                      gemv_rows_kernel<true, 4>,  gemv_rows_kernel<true, 8>};
+    constexpr uint32_t S = kRsDepthShort, L = kRsDepthLong;
+    static const Kernel kernels[16] = {
+        gemv_rows_kernel<false, 1, S>, gemv_rows_kernel<false, 2, S>, gemv_rows_kernel<false, 4, S>,
+        gemv_rows_kernel<false, 8, S>, gemv_rows_kernel<true, 1, S>,  gemv_rows_kernel<true, 2, S>,
+        gemv_rows_kernel<true, 4, S>,  gemv_rows_kernel<true, 8, S>,  gemv_rows_kernel<false, 1, L>,
+        gemv_rows_kernel<false, 2, L>, gemv_rows_kernel<false, 4, L>, gemv_rows_kernel<false, 8, L>,
+        gemv_rows_kernel<true, 1, L>,  gemv_rows_kernel<true, 2, L>,  gemv_rows_kernel<true, 4, L>,
+        gemv_rows_kernel<true, 8, L>};
     if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || p.kb < kGemvRsWaves || p.nseg == 0 || p.nseg > 4)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)kGemvRsWaves * gemv_rows_wave_lds(p.m);
     const uint32_t mt = p.m <= 1 ? 0 : p.m <= 2 ? 1 : p.m <= 4 ? 2 : 3;   // log2 of MT
-    hipLaunchKernelGGL(kernels[(p.x_vec ? 4 : 0) + mt], dim3(p.nctas), dim3(kGemvRsThreads), lds, stream, p);
+    const bool long_ring = p.m <= 2 && p.nctas <= cus;
+    hipLaunchKernelGGL(kernels[(long_ring ? 8 : 0) + (p.x_vec ? 4 : 0) + mt], dim3(p.nctas), dim3(kGemvRsThreads),
+                       lds, stream, p);
     return hipGetLastError();
 }
 

@@ -119,7 +119,8 @@ static_assert(kGemvRsMaxKb <= 64 * kGemvRsWaves, "a wavefront's block scales sit
 __host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 512 * stage_rows(m) + 16; }
 bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus);
 uint32_t gemv_rows_ctas(uint32_t rows);
-hipError_t launch_gemv_rows(const GemvParams &p, hipStream_t stream);
+// cus: compute units of the device (the ring depth depends on the rounds).
+hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, hipStream_t stream);
 
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup

@@ -310,7 +310,7 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
             cta += g.nctas;
         }
         p.nctas = cta;
-        HIP_TRY(launch_gemv_rows(p, st));
+        HIP_TRY(launch_gemv_rows(p, g_dev.cus, st));
         return Q35MM_OK;
     }
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
