@@ -158,7 +158,9 @@ namespace {
 constexpr uint32_t kBf16Tile = 64;                 // columns per tile
 constexpr uint32_t kBf16Stride = 144;              // LDS bytes per row
 constexpr uint32_t kBf16WaveLds = kBf16Tile * kBf16Stride + kBf16Tile * 4;
-constexpr uint32_t kBf16Depth = 3;                 // tiles in flight per wavefront
+// Tiles in flight per wavefront: with non-temporal weight loads two run
+// 1.5% faster than three or four on 248320 x 5120.
+constexpr uint32_t kBf16Depth = 2;
 }  // namespace
 
 __global__ __launch_bounds__(256) void bf16_gemv_vec_kernel(const uint16_t *__restrict__ w, uint32_t rows,
