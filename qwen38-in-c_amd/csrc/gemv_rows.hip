@@ -39,7 +39,8 @@ namespace q35mm {
 namespace {
 
 // K blocks in flight per wavefront (the ring depth DEPTH), chosen by the
-// host from the launch's shape; the summation order does not depend on it.
+// host from m and the launch's workgroup count; the summation order does
+// not depend on it, so results stay those of any other depth.
 // Three for a launch of one round of workgroups at m <= 2; two (fewer
 // registers: four wavefronts per SIMD instead of three) for launches of
 // several rounds, where more resident workgroups hide the latency, and for
