@@ -33,7 +33,7 @@ def sources() -> list[str]:
 def build_library(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *DEVICE_FLAGS, *COMMON_FLAGS, "-shared", "-Wl,-Bsymbolic", "-o", tmp, *sources()]
+    cmd = [HIPCC, *DEVICE_FLAGS, *COMMON_FLAGS, "-shared", "-Wl,-Bsymbolic-functions", "-o", tmp, *sources()]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

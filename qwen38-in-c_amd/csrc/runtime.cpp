@@ -811,11 +811,33 @@ __attribute__((constructor)) void lut_at_load() { fill_lut(q35_mm_fp8_lut); }
 // =====================================================================
 // Drop-in ABI (include/q35/q35_mm.h)
 // =====================================================================
+// The table's initial image is the decoded table itself (computed at compile
+// time), so every copy of it is right from the start: a C executable that
+// reads the table links it by copy relocation (the executable holds the
+// copy, initialised from this image, and the library, linked with
+// -Bsymbolic-functions only, binds its own references to that copy).
+namespace {
+constexpr uint32_t e4m3_const_bits(uint32_t v) {
+    const uint32_t sign = (v >> 7) << 31, e = (v >> 3) & 0xF, m = v & 7;
+    if (e == 0) return m ? sign | __builtin_bit_cast(uint32_t, (float)m * 0x1.0p-9f) : sign;
+    if (e == 15 && m == 7) return sign | 0x7FC00000u;
+    return sign | ((e + 120) << 23) | (m << 20);
+}
+constexpr float e4m3_const(uint32_t v) { return __builtin_bit_cast(float, e4m3_const_bits(v)); }
+}  // namespace
+#define Q35_LUT4(i) e4m3_const(i), e4m3_const(i + 1), e4m3_const(i + 2), e4m3_const(i + 3)
+#define Q35_LUT16(i) Q35_LUT4(i), Q35_LUT4(i + 4), Q35_LUT4(i + 8), Q35_LUT4(i + 12)
+#define Q35_LUT64(i) Q35_LUT16(i), Q35_LUT16(i + 16), Q35_LUT16(i + 32), Q35_LUT16(i + 48)
+
 // Braced linkage block: this is the definition of the exported data symbol
 // (the single-declaration form extern "C" T x; only declares it).
 extern "C" {
-__attribute__((visibility("default"))) float q35_mm_fp8_lut[256];
+__attribute__((visibility("default"))) float q35_mm_fp8_lut[256] = {Q35_LUT64(0), Q35_LUT64(64), Q35_LUT64(128),
+                                                                     Q35_LUT64(192)};
 }
+#undef Q35_LUT4
+#undef Q35_LUT16
+#undef Q35_LUT64
 
 Q35MM_API void q35_mm_init(void) {
     static std::once_flag once;

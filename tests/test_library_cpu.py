@@ -103,3 +103,33 @@ def test_python_wrapper_validates_shapes(q):
         q.mm_fp8(W, np.zeros((2, 2), np.uint16), np.zeros(20, np.float32))
     with pytest.raises(q.Q35mmError):
         q.mm_fp8(W.astype(np.int8), np.zeros((1, 1), np.uint16), np.zeros(20, np.float32))
+
+
+def test_lut_seen_by_a_linked_c_caller(q, oracle, tmp_path):
+    """A C program linked with -lq35mm (as the reference's model code links
+    its matmul) reads q35_mm_fp8_lut through a copy relocation; the table must
+    be right before and after q35_mm_init(), and the reference loader's
+    nearest-code search over it (qwen35-c/src/q35_model.c:41-57) must pick the
+    oracle's codes."""
+    import shutil
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not available")
+    exe = str(tmp_path / "lut_link")
+    libdir = os.path.dirname(q.LIB_PATH)
+    subprocess.run(["gcc", "-O1", "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "c", "lut_link.c"),
+                    "-o", exe, "-L", libdir, "-lq35mm", "-Wl,-rpath," + libdir, "-Wl,-rpath-link,/opt/rocm/lib",
+                    "-lm"], check=True, capture_output=True)
+    rel = subprocess.run(["readelf", "-r", exe], capture_output=True, text=True, check=True).stdout
+    assert "q35_mm_fp8_lut" in rel   # the executable holds the table's copy
+    vals = np.array([1.0, -3.3, 0.0017, 500.0, -448.0, 1e-6, 0.0009765625, 0.0029296875, 240.0, 232.0,
+                     -0.013671875, 0.0], np.float32)
+    out = subprocess.run([exe] + [repr(float(v)) for v in vals], capture_output=True, text=True,
+                         check=True).stdout.split("\n")
+    want = oracle.lut().view(np.uint32)
+    for line, tag in zip(out[:2], ("before", "after")):
+        words = line.split()
+        assert words[0] == tag
+        got = np.array([int(w, 16) for w in words[1:]], np.uint32)
+        assert (got == want).all(), f"table {tag} q35_mm_init differs from the oracle"
+    codes = [int(c) for c in out[2].split()[1:]]
+    assert codes == [int(oracle.lib.orc_f32_to_e4m3(float(v))) for v in vals]
