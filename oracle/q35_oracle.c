@@ -13,6 +13,8 @@
 #include "q35_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #if defined(_OPENMP)
@@ -208,6 +210,18 @@ static float dot_row(const uint8_t *wr, const float *srow, uint32_t cols,
     return sum;
 }
 
+/* A thread's buffer for one widened scale row (kb floats); aborts when the
+ * allocation fails, so no caller ever runs on a short buffer. */
+static float *scale_row_alloc(uint32_t kb)
+{
+    float *p = (float *)malloc((size_t)(kb ? kb : 1u) * sizeof(float));
+    if (!p) {
+        fprintf(stderr, "oracle: out of memory for a scale row of %u blocks\n", kb);
+        abort();
+    }
+    return p;
+}
+
 /* Widened scale row for weight row r: s[r/128][*] as fp32. */
 static void scale_row_bf16(const uint16_t *sc, uint32_t r, uint32_t kb, float *srow)
 {
@@ -222,7 +236,7 @@ void orc_mm_fp8_batch(const uint8_t *W, const uint16_t *scale_bf16,
     uint32_t kb = (cols + 127u) / 128u;
     #pragma omp parallel
     {
-        float srow[1024];   /* cols <= 131072 */
+        float *srow = scale_row_alloc(kb);
         #pragma omp for schedule(static)
         for (int64_t r = 0; r < (int64_t)rows; r++) {
             scale_row_bf16(scale_bf16, (uint32_t)r, kb, srow);
@@ -230,6 +244,7 @@ void orc_mm_fp8_batch(const uint8_t *W, const uint16_t *scale_bf16,
                 Y[(size_t)t * rows + (size_t)r] =
                     dot_row(W + (size_t)r * cols, srow, cols, X + (size_t)t * cols);
         }
+        free(srow);
     }
 }
 
@@ -258,7 +273,7 @@ void orc_mm_fp8_rows(const uint8_t *W, const uint16_t *scale_bf16,
     uint32_t kb = (cols + 127u) / 128u;
     #pragma omp parallel
     {
-        float srow[1024];
+        float *srow = scale_row_alloc(kb);
         #pragma omp for schedule(static)
         for (int64_t i = 0; i < (int64_t)nidx; i++) {
             uint32_t r = row_idx[i];
@@ -267,6 +282,7 @@ void orc_mm_fp8_rows(const uint8_t *W, const uint16_t *scale_bf16,
                 Y[(size_t)t * nidx + (size_t)i] =
                     dot_row(W + (size_t)r * cols, srow, cols, X + (size_t)t * cols);
         }
+        free(srow);
     }
 }
 
