@@ -6,24 +6,35 @@
 // the shapes gemv_rows_shape() selects, e.g. 5120->6144, 4096->5120,
 // 5120->17408 and 17408->5120.
 //
-// Decomposition.  One workgroup per 32-row sub-tile (the weight's
-// ceil(rows/32) sub-tiles fill at least half of the CUs), and the
-// workgroup's kGemvRsWaves wavefronts split K into contiguous ranges of K
-// blocks.  Each wavefront streams its range of the sub-tile (4 KiB per K
-// block, one 16-byte load per lane per 1 KiB chunk) through a ring of
-// DEPTH blocks; the wavefront partials are added through LDS in
-// wavefront order at the end.  No partial output leaves the workgroup, so
-// there are no tickets, no workspace and no second pass: that is the whole
-// point against stream-K, whose split-group protocol costs a few
-// microseconds per launch, as much as streaming these weights takes.
+// Decomposition.  Each workgroup owns a range of at most 32 consecutive
+// rows of one weight, and its NW (4 or 8) wavefronts split K into
+// contiguous ranges of K blocks.  Each wavefront streams its K range of
+// those rows (lane l loads row r0 + l%32 of the lane-order tiles, 16 bytes
+// per 32-column chunk) through a ring of DEPTH blocks; the wavefront
+// partials are added through LDS in wavefront order at the end.  No partial
+// output leaves the workgroup, so there are no tickets, no workspace and no
+// second pass: that is the whole point against stream-K, whose split-group
+// protocol costs a few microseconds per launch, as much as streaming these
+// weights takes.
 //
+// Ranges (gemv_rows_plan).  A launch whose weights hold at least half as
+// many 32-row sub-tiles as the device has CUs runs one workgroup per
+// sub-tile: each load is a whole 1 KiB chunk, which the memory system
+// streams fastest (a raw-read probe of 5120 x 17408 codes: 15.2 us as
+// sub-tiles on 160 CUs against 17.5 us as 256 ranges of 20 rows, whose
+// loads read 320-byte pieces of each chunk).  Smaller launches (the
+// model's 1024-row k/v projections, 48-row DeltaNet gates) would leave most
+// CUs idle that way; they get one workgroup per CU, each a balanced range
+// of whole 4-row quads (which may straddle sub-tiles and scale groups).
+
 // Arithmetic is the stream-K kernel's: e4m3 -> bf16 exactly, activations
 // split exactly into three bf16 parts (A-operand rows m = token + 8*part),
-// v_mfma_f32_32x32x16_bf16 per K block, the block's fp32 scale applied with
-// one fmaf per output.  The summation order depends only on the shape (K
-// ranges per wavefront, wavefronts in order), so a batch of m tokens gives
-// exactly the bits of m single-token calls, and a weight gives the same
-// bits alone or in a multi-weight launch.
+// v_mfma_f32_32x32x16_bf16 per K block (weight row r0 + n is MFMA column
+// n), the block's fp32 scale applied with one fmaf per output.  A row's
+// summation order depends only on K (K ranges per wavefront, wavefronts in
+// order), not on which range holds it, so a batch of m tokens gives exactly
+// the bits of m single-token calls, and a weight gives the same bits alone
+// or in a multi-weight launch.
 //
 // Activations.  Each K block's activations ride the weight ring one block
 // ahead: the slot that brings the weights of block b brings the activations
@@ -31,6 +42,8 @@
 // in LDS while block b's MFMAs run.  Nothing is staged up front and no
 // barrier is needed before the stream: each wavefront only reads LDS it
 // wrote itself (LDS operations of one wavefront complete in order).
+#include <algorithm>
+
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
 
@@ -130,26 +143,37 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
 
 }  // namespace
 
-// MT = m rounded up to a power of two; DEPTH = ring depth.
-template <bool VEC, uint32_t MT, uint32_t DEPTH>
-__global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p) {
+// MT = m rounded up to a power of two; DEPTH = ring depth; NW = wavefronts.
+template <bool VEC, uint32_t MT, uint32_t DEPTH, uint32_t NW>
+__global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float red[kGemvRsWaves][kGemvMaxM][kSubRows];
+    __shared__ float red[NW][kGemvMaxM][kSubRows];
 
     uint32_t si = 0;
 #pragma unroll
     for (uint32_t i = 1; i < 4; i++)
         if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
     const GemvSeg &sg = p.seg[si];
-    const uint32_t sub = blockIdx.x - sg.cta_begin;   // 32-row sub-tile
-    const uint32_t g = sub >> 2, s = sub & 3;
+    // Rows [r0, r1) of the segment: unit_rows rows per workgroup, or quads
+    // [c*Q/P, (c+1)*Q/P) of its Q quads over its P workgroups (the host keeps
+    // P <= Q and ceil(Q/P) <= 8).
+    const uint32_t c = blockIdx.x - sg.cta_begin;
+    uint32_t r0, r1;
+    if (sg.unit_rows) {
+        r0 = c * sg.unit_rows;
+        r1 = min(r0 + sg.unit_rows, sg.rows);
+    } else {
+        const uint32_t Q = (sg.rows + 3) >> 2, P = sg.nctas;
+        r0 = 4 * (uint32_t)((uint64_t)c * Q / P);
+        r1 = min(4 * (uint32_t)((uint64_t)(c + 1) * Q / P), sg.rows);
+    }
     const uint32_t KB = p.kb, M = p.m, R = stage_rows(M);
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // K blocks of this wavefront: kbof(i) = k0 + i for i < n (KB >= waves).
     // (Interleaving the wavefronts over K instead measured the same.)
-    const uint32_t k0 = wv * KB / kGemvRsWaves, n = (wv + 1) * KB / kGemvRsWaves - k0;
+    const uint32_t k0 = wv * KB / NW, n = (wv + 1) * KB / NW - k0;
     auto kbof = [&](uint32_t i) { return k0 + i; };
 
     // This wavefront's LDS: two A-operand slots and a 16-byte zero slot.
@@ -164,16 +188,25 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
     const uint32_t a_step = a_active ? R * 32 : 0;
     if (lane < 4) reinterpret_cast<uint32_t *>(wbase + 512 * R)[lane] = 0u;
 
-    // ---- block scales: lane i holds the scale of block kbof(i) (a range has
-    // at most 64 blocks); v_readlane picks it per block, so no scalar load
-    // shares the LDS counter with the operand reads inside the loop ----
-    const float sc_lane = sg.scale[(size_t)g * KB + kbof(min(lane, n - 1))];
+    // ---- block scales of the (at most two) 128-row groups the range
+    // touches: lane i holds block kbof(i)'s (a wavefront has at most 64
+    // blocks); v_readlane picks them per block, so no scalar load shares the
+    // LDS counter with the operand reads inside the loop.  An output lane
+    // (column mrow = row r0 + mrow) takes its row's group ----
+    const uint32_t ga = r0 >> 7, gb = (r1 - 1) >> 7;
+    const float sca_lane = sg.scale[(size_t)ga * KB + kbof(min(lane, n - 1))];
+    const float scb_lane = sg.scale[(size_t)gb * KB + kbof(min(lane, n - 1))];
+    const bool out_in_a = ((r0 + mrow) >> 7) == ga;
 
     // ---- ring: slot d holds the weights of block b and the activations of
     // block b+1 (clamped into the range).  Weights are read once per call:
     // non-temporal loads keep them from displacing cached data (layer step
     // +3.4% against plain loads) ----
-    const uint8_t *codes = sg.codes + (size_t)g * KB * kBlockBytes + s * kSubBytes + lane * 16;
+    // lane l: row r0 + l%32 (clamped into the range; the extra columns are
+    // never written), its sub-tile and place in the 1 KiB chunks
+    const uint32_t rl = min(r0 + mrow, r1 - 1);
+    const uint8_t *codes = sg.codes + ((size_t)(rl >> 7) * KB * 4 + ((rl >> 5) & 3)) * kSubBytes + hh * 512 +
+                           (rl & 31) * 16;
     u32x4_t buf[DEPTH][4];
     XBlock<MT> xr[DEPTH];
     auto load = [&](uint32_t d, uint32_t i) {
@@ -218,8 +251,11 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
                         const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, araw[j * 2 + q]);
                         part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
                     }
-                const float sc =
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), bb));
+                const float sca =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sca_lane), bb));
+                const float scb =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scb_lane), bb));
+                const float sc = out_in_a ? sca : scb;
                 // acc[r + 4p] holds part p of token 4h + (r & 3): only tokens
                 // below MT are scaled; rows 24..31 carry nothing (regs 12..15)
 #pragma unroll
@@ -242,41 +278,72 @@ __global__ __launch_bounds__(kGemvRsThreads) void gemv_rows_kernel(GemvParams p)
         const uint32_t t = threadIdx.x >> 5, n = threadIdx.x & 31;
         float sum = red[0][t][n];
 #pragma unroll
-        for (uint32_t w = 1; w < kGemvRsWaves; w++) sum += red[w][t][n];
-        const uint32_t row = g * kBlock + s * kSubRows + n;
-        if (row < sg.rows) {
+        for (uint32_t w = 1; w < NW; w++) sum += red[w][t][n];
+        const uint32_t row = r0 + n;
+        if (row < r1) {
             const size_t o = (size_t)t * sg.ldy + row;
             sg.y[o] = sg.resid ? sg.resid[o] + sum : sum;
         }
     }
 }
 
-bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus) {
-    const uint32_t nsub = (rows + kSubRows - 1) / kSubRows;
-    // No upper bound on rows: a launch of several rounds of workgroups
-    // (5120 -> 2 x 17408: 1088 workgroups) still beats stream-K at m = 1.
-    return 2 * nsub >= cus && kb >= 2 * kGemvRsWaves && kb <= kGemvRsMaxKb;
+bool gemv_rows_shape(uint32_t kb, uint32_t waves) { return kb >= waves && kb <= kGemvRsMaxKb && kb <= 64 * waves; }
+
+void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t cus, uint32_t *nctas, uint32_t *unit_rows) {
+    uint64_t tot = 0, subs = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        tot += rows[s];
+        subs += (rows[s] + kSubRows - 1) / kSubRows;
+    }
+    for (uint32_t s = 0; s < nseg; s++) {
+        if (2 * subs >= cus) {
+            nctas[s] = (rows[s] + kSubRows - 1) / kSubRows;
+            unit_rows[s] = kSubRows;
+            continue;
+        }
+        const uint64_t q = (rows[s] + 3) / 4;
+        uint64_t ps = tot ? (uint64_t)cus * rows[s] / tot : 1;
+        ps = std::max<uint64_t>(ps, (q + 7) / 8);   // at most 8 quads = 32 rows each
+        ps = std::min<uint64_t>(ps, q);             // every range holds a quad
+        nctas[s] = (uint32_t)std::max<uint64_t>(ps, 1);
+        unit_rows[s] = 0;
+    }
 }
 
-uint32_t gemv_rows_ctas(uint32_t rows) { return (rows + kSubRows - 1) / kSubRows; }
+namespace {
+using RowsKernel = void (*)(GemvParams);
 
-hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, hipStream_t stream) {
-    using Kernel = void (*)(GemvParams);
-    constexpr uint32_t S = kRsDepthShort, L = kRsDepthLong;
-    static const Kernel kernels[16] = {
-        gemv_rows_kernel<false, 1, S>, gemv_rows_kernel<false, 2, S>, gemv_rows_kernel<false, 4, S>,
-        gemv_rows_kernel<false, 8, S>, gemv_rows_kernel<true, 1, S>,  gemv_rows_kernel<true, 2, S>,
-        gemv_rows_kernel<true, 4, S>,  gemv_rows_kernel<true, 8, S>,  gemv_rows_kernel<false, 1, L>,
-        gemv_rows_kernel<false, 2, L>, gemv_rows_kernel<false, 4, L>, gemv_rows_kernel<false, 8, L>,
-        gemv_rows_kernel<true, 1, L>,  gemv_rows_kernel<true, 2, L>,  gemv_rows_kernel<true, 4, L>,
-        gemv_rows_kernel<true, 8, L>};
-    if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || p.kb < kGemvRsWaves || p.nseg == 0 || p.nseg > 4)
+template <uint32_t NW>
+RowsKernel rows_kernel(uint32_t depth, uint32_t vec_mt) {
+#define Q35_RK(D)                                                                                          \
+    {gemv_rows_kernel<false, 1, D, NW>, gemv_rows_kernel<false, 2, D, NW>, gemv_rows_kernel<false, 4, D, NW>, \
+     gemv_rows_kernel<false, 8, D, NW>, gemv_rows_kernel<true, 1, D, NW>,  gemv_rows_kernel<true, 2, D, NW>,  \
+     gemv_rows_kernel<true, 4, D, NW>,  gemv_rows_kernel<true, 8, D, NW>}
+    static const RowsKernel k[3][8] = {Q35_RK(2), Q35_RK(3), Q35_RK(4)};
+#undef Q35_RK
+    return k[depth - 2][vec_mt];
+}
+}  // namespace
+
+hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, uint32_t waves, uint32_t depth, hipStream_t stream) {
+    if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || (waves != 4 && waves != 8) ||
+        !gemv_rows_shape(p.kb, waves) || p.nseg == 0 || p.nseg > 4)
         return hipErrorInvalidValue;
-    const size_t lds = (size_t)kGemvRsWaves * gemv_rows_wave_lds(p.m);
+    for (uint32_t s = 0; s < p.nseg; s++) {
+        const GemvSeg &g = p.seg[s];
+        const uint32_t q = (g.rows + 3) / 4;
+        const bool ok = g.unit_rows ? g.unit_rows <= kSubRows && (uint64_t)g.nctas * g.unit_rows >= g.rows &&
+                                          (uint64_t)(g.nctas - 1) * g.unit_rows < g.rows
+                                    : g.nctas > 0 && g.nctas <= q && (q + g.nctas - 1) / g.nctas <= 8;
+        if (!ok) return hipErrorInvalidValue;   // every range must hold 1..32 rows
+    }
+    const size_t lds = (size_t)waves * gemv_rows_wave_lds(p.m);
     const uint32_t mt = p.m <= 1 ? 0 : p.m <= 2 ? 1 : p.m <= 4 ? 2 : 3;   // log2 of MT
-    const bool long_ring = p.m <= 2 && p.nctas <= cus;
-    hipLaunchKernelGGL(kernels[(long_ring ? 8 : 0) + (p.x_vec ? 4 : 0) + mt], dim3(p.nctas), dim3(kGemvRsThreads),
-                       lds, stream, p);
+    if (depth == 0) depth = p.m <= 2 && p.nctas <= cus ? kRsDepthLong : kRsDepthShort;
+    depth = std::min(std::max(depth, 2u), 4u);
+    const uint32_t vm = (p.x_vec ? 4 : 0) + mt;
+    const RowsKernel k = waves == 8 ? rows_kernel<8>(depth, vm) : rows_kernel<4>(depth, vm);
+    hipLaunchKernelGGL(k, dim3(p.nctas), dim3(64 * waves), lds, stream, p);
     return hipGetLastError();
 }
 

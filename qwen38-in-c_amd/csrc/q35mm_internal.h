@@ -52,6 +52,7 @@ struct GemvSeg {
     uint32_t maxc;       // contributions per group the workspace holds
     uint32_t ws_off;     // float offset of the segment's partials [nb][maxc][8][128]
     uint32_t cnt_off;    // offset of the segment's arrival counters [nb]
+    uint32_t unit_rows;  // row-split GEMV: rows per workgroup (0: balanced 4-row quads)
 };
 
 // What the staged activations are, per column k of token t:
@@ -101,26 +102,32 @@ uint32_t gemv_norm_cols(uint32_t k);
 size_t gemv_norm_lds_bytes(uint32_t m, uint32_t norm_cols);
 hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 
-// Row-split decode GEMV (gemv_rows.hip): one workgroup per 32-row sub-tile,
-// kGemvRsWaves wavefronts splitting K, no partial outputs between
-// workgroups.  Used for the weights gemv_rows_shape() selects (by shape only,
-// so batch and multi-weight results stay those of single calls); activations
-// plain (kXPlain), optional residual.  Segments: cta_begin / nctas =
-// gemv_rows_ctas(rows); ws, cnt, max_range unused.
-constexpr uint32_t kGemvRsWaves = 4;
-constexpr uint32_t kGemvRsThreads = 64 * kGemvRsWaves;
-// Every row-split workgroup splits all m*K activations itself, so that
-// redundant work grows with K*m: at 136 K blocks (17408 columns) row-split
-// still wins for m <= 4 and loses ~10% at m = 8; beyond 160 blocks
-// stream-K is kept.
+// Row-split decode GEMV (gemv_rows.hip): each workgroup owns a range of at
+// most 32 rows of one weight, its wavefronts (4 or 8) splitting K; no
+// partial outputs between workgroups.  Used for the weights
+// gemv_rows_shape() selects (by K only, so batch and multi-weight results
+// stay those of single calls); activations plain (kXPlain), optional
+// residual.  Segments: nctas and unit_rows from gemv_rows_plan (cta_begin
+// consecutive); ws, cnt, max_range unused.
+constexpr uint32_t kGemvRsMaxWaves = 8;
+// Every row-split workgroup splits all m*K activations of its wavefronts'
+// K ranges itself, so that redundant work grows with K*m; beyond 160 K
+// blocks stream-K is kept.
 constexpr uint32_t kGemvRsMaxKb = 160;
-static_assert(kGemvRsMaxKb <= 64 * kGemvRsWaves, "a wavefront's block scales sit one per lane");
 // Per wavefront: two A-operand slots of 256 * stage_rows(m) bytes + a zero slot.
 __host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 512 * stage_rows(m) + 16; }
-bool gemv_rows_shape(uint32_t rows, uint32_t kb, uint32_t cus);
-uint32_t gemv_rows_ctas(uint32_t rows);
-// cus: compute units of the device (the ring depth depends on the rounds).
-hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, hipStream_t stream);
+// K blocks and wavefronts per workgroup the kernel accepts (a wavefront's
+// block scales sit one per lane: at most 64 blocks each).
+bool gemv_rows_shape(uint32_t kb, uint32_t waves);
+// Workgroups and rows per workgroup for one launch over weights of
+// rows[0..nseg) rows.  Weights of at least cus/2 32-row sub-tiles in all
+// run one workgroup per sub-tile (unit_rows = 32: whole 1 KiB chunks per
+// load, which the memory system streams fastest); smaller launches get cus
+// workgroups shared in proportion to the rows, each a balanced range of
+// whole 4-row quads (unit_rows = 0), so every CU streams.
+void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t cus, uint32_t *nctas, uint32_t *unit_rows);
+// waves: 4 or 8; depth: ring depth 2..4 (0: by launch shape).
+hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, uint32_t waves, uint32_t depth, hipStream_t stream);
 
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup

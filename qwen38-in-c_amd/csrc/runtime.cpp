@@ -94,6 +94,8 @@ struct Device {
     bool trust_pointers = false;
     bool mlp_unfused = false;   // Q35MM_MLP_UNFUSED=1: separate neighbour kernels on the GEMV path
     bool gemv_rows = true;      // Q35MM_GEMV_ROWSPLIT=0: every weight on the stream-K GEMV
+    uint32_t rows_depth = 0;    // Q35MM_ROWS_DEPTH: ring depth of the row-split GEMV (0: by launch)
+    uint32_t rows_waves = 4;    // Q35MM_ROWS_WAVES: wavefronts per row-split workgroup (4 or 8)
 };
 
 std::recursive_mutex g_mu;
@@ -120,6 +122,8 @@ int ensure_device() {
     g_dev.cus = (uint32_t)prop.multiProcessorCount;
     g_dev.gemv_per_cu = std::max(1u, env_u32("Q35MM_GEMV_CTAS_PER_CU", kGemvCtasPerCu));
     g_dev.gemv_rows = env_u32("Q35MM_GEMV_ROWSPLIT", 1) != 0;
+    g_dev.rows_depth = env_u32("Q35MM_ROWS_DEPTH", 0);
+    g_dev.rows_waves = env_u32("Q35MM_ROWS_WAVES", 4) == 8 ? 8 : 4;
     return Q35MM_OK;
 }
 
@@ -272,7 +276,13 @@ constexpr uint32_t kMlpFusedSwiGLUMaxM = 2;
 
 // Which decode GEMV a weight runs on; fixed by its shape (and the device),
 // never by m or by the other weights of a call.
-bool uses_gemv_rows(const Weight &w) { return g_dev.gemv_rows && gemv_rows_shape(w.rows, w.kb, g_dev.cus); }
+enum GemvKind : uint32_t { kStreamK = 0, kRows = 1 };
+
+uint32_t gemv_kind(const Weight &w) {
+    return g_dev.gemv_rows && gemv_rows_shape(w.kb, g_dev.rows_waves) ? kRows : kStreamK;
+}
+
+bool uses_gemv_rows(const Weight &w) { return gemv_kind(w) != kStreamK; }
 
 int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
                    float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid) {
@@ -291,10 +301,13 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     p.nseg = nseg;
     p.x_vec = (aligned16(dX) && cols % 8 == 0 && (!in.x2 || aligned16(in.x2)) &&
                (!in.norm_w || aligned16(in.norm_w))) ? 1u : 0u;
-    if (uses_gemv_rows(w[0]->w)) {
+    const uint32_t kind = gemv_kind(w[0]->w);
+    if (kind != kStreamK) {
         // the callers keep row-split weights on plain activations
         if (in.xmode != kXPlain) return set_error(Q35MM_EINVAL, "row-split GEMV takes plain activations");
-        uint32_t cta = 0;
+        uint32_t cta = 0, rows[4], nct[4], urows[4];
+        for (uint32_t s = 0; s < nseg; s++) rows[s] = w[s]->w.rows;
+        gemv_rows_plan(rows, nseg, g_dev.cus, nct, urows);
         for (uint32_t s = 0; s < nseg; s++) {
             const Weight &ws = w[s]->w;
             GemvSeg &g = p.seg[s];
@@ -306,11 +319,12 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
             g.ldy = ws.rows;
             g.nb = ws.nb;
             g.cta_begin = cta;
-            g.nctas = gemv_rows_ctas(ws.rows);
+            g.nctas = nct[s];
+            g.unit_rows = urows[s];
             cta += g.nctas;
         }
         p.nctas = cta;
-        HIP_TRY(launch_gemv_rows(p, g_dev.cus, st));
+        HIP_TRY(launch_gemv_rows(p, g_dev.cus, g_dev.rows_waves, g_dev.rows_depth, st));
         return Q35MM_OK;
     }
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
@@ -358,12 +372,12 @@ int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const floa
         const uint32_t mg = std::min(kGemvMaxM, m - t0);
         GemvInput ig = in;
         if (ig.x2) ig.x2 += (size_t)t0 * cols;
-        for (int rows_split = 0; rows_split < 2; rows_split++) {
+        for (uint32_t kind = kStreamK; kind <= kRows; kind++) {
             const q35mm_weight *wg[4];
             float *ys[4], *rs[4];
             uint32_t n = 0;
             for (uint32_t s = 0; s < nseg; s++) {
-                if (uses_gemv_rows(w[s]->w) != (rows_split != 0)) continue;
+                if (gemv_kind(w[s]->w) != kind) continue;
                 wg[n] = w[s];
                 ys[n] = dY[s] + (size_t)t0 * w[s]->w.rows;
                 rs[n] = resid ? resid[s] + (size_t)t0 * w[s]->w.rows : nullptr;
