@@ -133,57 +133,130 @@ def measured_traffic(profile: str):
     return None
 
 
-def cpu_baseline(wl, base, budget_s: float = 12.0):
-    """The reference's compiled q35_mm.c (AVX2 + OpenMP), or the oracle port
-    if the reference build is absent, on one layer at M=1."""
+def host_cpu_info() -> dict:
+    """The host's CPU as lscpu reports it (the whole machine, not this
+    process's share)."""
+    info = {"model": "unknown", "sockets": None, "cores_per_socket": None, "threads_per_core": None,
+            "numa_nodes": None, "logical_cpus": os.cpu_count()}
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "NUMA node(s)": "numa_nodes"}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for ln in out.splitlines():
+            k, _, v = ln.partition(":")
+            if k.strip() in keys:
+                v = v.strip()
+                info[keys[k.strip()]] = int(v) if v.isdigit() else v
+    except Exception:
+        try:
+            for ln in open("/proc/cpuinfo"):
+                if ln.startswith("model name"):
+                    info["model"] = ln.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return info
+
+
+CPU_CHILD = "--cpu-child"
+
+
+def cpu_child(budget_s: float) -> None:
+    """The CPU baseline, run in a child process (no torch, no GPU) so that
+    OMP_NUM_THREADS / OMP_PROC_BIND apply to the OpenMP runtime the
+    reference's matmul starts: the reference's compiled q35_mm.c
+    (oracle/_ref, AVX2 + FMA + OpenMP), or the oracle port if that build is
+    absent, on the GPU workloads' inputs (same seeds).  Prints one JSON line."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from oracle import REF_PATH, Oracle, RefMM
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    if RefMM.available():
-        impl, kind = RefMM(), "reference"
-        run = impl.mm
-    else:
-        impl, kind = Oracle(), "port"
-        run = impl.mm
+    import workload as wl
+    from oracle import Oracle, RefMM
+    ref = RefMM.available()
+    impl = RefMM() if ref else Oracle()
+    kind = "reference" if ref else "port"
+
+    def med_time(fn, budget, at_least=3, at_most=200):
+        fn()   # warm: page in, start the threads
+        times, t_end = [], time.time() + budget
+        while time.time() < t_end or len(times) < at_least:
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+            if len(times) >= at_most:
+                break
+        return float(np.median(times)), len(times)
+
+    out = {"kind": kind, "threads": int(os.environ.get("OMP_NUM_THREADS", "0") or 0),
+           "omp_proc_bind": os.environ.get("OMP_PROC_BIND"), "omp_places": os.environ.get("OMP_PLACES")}
+    # one layer's decode projections at M = 1, gate and up through multi4 as
+    # the reference's decode calls them (qwen35-c/src/q35_model.c:930-937)
+    base = []
+    for i, (name, k, n) in enumerate(wl.DECODE_SHAPES):
+        W, sc = wl.gen_weight(wl.SEED_BASE + 1 + 16 * i, n, k)
+        base.append((name, k, n, W, sc))
     xs = [wl.gen_act(7 + i, 1, k)[0] for i, (_, k, _, _, _) in enumerate(base)]
-    xs[3] = xs[2]                      # gate and up share x
-    layer_bytes = sum(wl.algorithmic_bytes(1, k, n) for _, k, n, _, _ in base)
+    xs[3] = xs[2]
 
     def layer():
-        # as the reference's decode: gate and up in one multi4 call
         for j in (0, 1):
-            run(base[j][3], base[j][4], xs[j])
-        if kind == "reference":
+            impl.mm(base[j][3], base[j][4], xs[j])
+        if ref:
             impl.multi4([base[2][3], base[3][3]], [base[2][4], base[3][4]], xs[2])
         else:
-            run(base[2][3], base[2][4], xs[2])
-            run(base[3][3], base[3][4], xs[3])
-        run(base[4][3], base[4][4], xs[4])
-    layer()   # warm: page in, spin up threads
-    times = []
-    t_end = time.time() + budget_s
-    while time.time() < t_end or len(times) < 3:
-        t = time.perf_counter()
-        layer()
-        times.append(time.perf_counter() - t)
-        if len(times) >= 200:
-            break
-    med = float(np.median(times))
-    cpu = "unknown"
-    try:
-        for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                cpu = ln.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(layer_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{len(times)} passes of one layer's 5 projections at M=1 (gate+up via multi4) "
-                      f"({layer_bytes / 1e6:.1f} MB), median {med * 1e3:.2f} ms/pass; "
-                      f"{'oracle/_ref q35_mm.c' if kind == 'reference' else 'oracle port'}, "
-                      f"OMP_NUM_THREADS={threads}, host CPU: {cpu}"}
+            impl.mm(base[2][3], base[2][4], xs[2])
+            impl.mm(base[3][3], base[3][4], xs[3])
+        impl.mm(base[4][3], base[4][4], xs[4])
+    lb = sum(wl.algorithmic_bytes(1, k, n) for _, k, n, _, _ in base)
+    t, cnt = med_time(layer, budget_s)
+    out["layer"] = {"GBps": round(lb / t / 1e9, 3), "ms": round(t * 1e3, 3), "passes": cnt, "bytes": lb}
+    del base
+    # configuration 0: one 5120 x 5120 GEMV
+    _, k, n = wl.SINGLE_SHAPE
+    W, sc = wl.gen_weight(wl.SEED_BASE + 0, n, k)
+    x = wl.gen_act(wl.SEED_BASE + 0x100, 1, k)[0]
+    t, cnt = med_time(lambda: impl.mm(W, sc, x), budget_s / 4)
+    b0 = wl.algorithmic_bytes(1, k, n)
+    out["single"] = {"GBps": round(b0 / t / 1e9, 3), "ms": round(t * 1e3, 3), "passes": cnt}
+    del W
+    # the prefill GEMM shapes on a sample of the 512 tokens (bf16-representable)
+    mt = 64
+    pre = {"tokens": mt}
+    tot_f, tot_t = 0, 0.0
+    for i, (name, k, n) in enumerate(wl.PREFILL_SHAPES):
+        W, sc = wl.gen_weight(wl.SEED_BASE + 2 + 32 * i, n, k)
+        X = wl.gen_act(wl.SEED_BASE + 3 + i, 512, k, bf16=True)[:mt].copy()
+        t, cnt = med_time(lambda: impl.mm_batch(W, sc, X), 0.0, at_least=2, at_most=2)
+        f = wl.flops(mt, k, n)
+        pre[name] = {"ms": round(t * 1e3, 2), "TFLOPs": round(f / t / 1e12, 4)}
+        tot_f += f
+        tot_t += t
+        del W
+    pre["TFLOPs"] = round(tot_f / tot_t / 1e12, 4)
+    out["prefill_sample"] = pre
+    print(json.dumps(out), flush=True)
 
+
+def cpu_baseline(budget_s: float = 12.0):
+    """Runs cpu_child in a child process on this host's CPU share:
+    OMP_NUM_THREADS from the environment (the box's share) or the visible
+    CPUs, threads bound close to their cores."""
+    import subprocess
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    res = subprocess.run([sys.executable, os.path.abspath(__file__), CPU_CHILD, str(budget_s)], env=env,
+                         capture_output=True, text=True, timeout=900)
+    if res.returncode != 0:
+        raise RuntimeError("CPU baseline child failed:\n" + res.stderr[-3000:])
+    out = json.loads(res.stdout.strip().splitlines()[-1])
+    host = host_cpu_info()
+    phys = (host.get("sockets") or 1) * (host.get("cores_per_socket") or 0)
+    if isinstance(phys, int) and phys > 0:
+        # the reference CLI's own default: min(5/3 x physical cores, OpenMP's maximum)
+        # (qwen35-c/src/cli/cli_common.c:96-105), computed for the whole host
+        out["reference_auto_threads"] = min(phys * 5 // 3, host.get("logical_cpus") or phys * 5 // 3)
+    out["host"] = host
+    return out
 
 def write_safetensors(path: str, tensors) -> int:
     """tensors: (name, dtype, shape, numpy array); returns bytes written."""
@@ -199,6 +272,116 @@ def write_safetensors(path: str, tensors) -> int:
         for _, _, _, arr in tensors:
             f.write(np.ascontiguousarray(arr).tobytes())
     return 8 + len(h) + off
+
+
+def variant_pool(q, wl, seed, n, k, copies):
+    """copies distinct resident weights of one shape: a generated weight and
+    its row-sign variants (row_sign_mask)."""
+    W, sc = wl.gen_weight(seed, n, k)
+    return [q.Weight(W if v == 0 else (W ^ row_sign_mask(n, v)), sc) for v in range(copies)]
+
+
+def bench_single(q, wl, torch, dev, steps, warmup, use_graph, pool_bytes=1 << 30):
+    """Configuration 0: one 5120 x 5120 GEMV at M = 1, calls rotating over
+    distinct resident copies totalling at least pool_bytes (more than the 256
+    MB Infinity Cache and the L2s can hold)."""
+    _, k, n = wl.SINGLE_SHAPE
+    copies = max(8, -(-pool_bytes // (n * k)))
+    ws = variant_pool(q, wl, wl.SEED_BASE + 0, n, k, copies)
+    x = torch.from_numpy(wl.gen_act(wl.SEED_BASE + 0x100, 1, k)).to(dev)
+    y = torch.empty((1, n), device=dev)
+
+    def call(i):
+        q.gemv(ws[i % copies], x, y, m=1)
+    el, g = time_graph(torch, call, steps, warmup, use_graph)
+    del g
+    b = wl.algorithmic_bytes(1, k, n)
+    us = el / steps * 1e6
+    for w in ws:
+        w.free()
+    return {"m": 1, "k": k, "n": n, "copies": copies, "pool_MB": round(copies * n * k / 1e6, 1),
+            "calls": steps, "us": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": b}
+
+
+def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
+    """One decode token of the reference model at M = 1, in its call order:
+    per layer the DeltaNet multi4 (in_proj_qkv, in_proj_z, in_proj_a,
+    in_proj_b) and out_proj, or the GQA q, k, v and o_proj, then the MLP's
+    gate+up multi4 and down (qwen35-c/src/q35_model.c:903-937,
+    qwen35-c/src/q35_deltanet.c:325-329,360, qwen35-c/src/q35_attn.c:262,
+    273-275): 48 x 4 + 16 x 6 = 288 launches.  Every layer's weights are
+    distinct and resident (the MLP weights are the stack's)."""
+    n_dn = sum(1 for i in range(layers) if not wl.model_layer_is_gqa(i))
+    t0 = time.time()
+    dn = [variant_pool(q, wl, wl.SEED_BASE + 0x60 + j, n, k, n_dn)
+          for j, (_, k, n) in enumerate(wl.MODEL_DELTANET_SHAPES)]
+    gq = [variant_pool(q, wl, wl.SEED_BASE + 0x70 + j, n, k, layers - n_dn)
+          for j, (_, k, n) in enumerate(wl.MODEL_GQA_SHAPES)]
+    log(f"model token: {n_dn} DeltaNet + {layers - n_dn} GQA layers of projections resident "
+        f"in {time.time() - t0:.1f}s")
+    xs = {k: torch.randn(1, k, device=dev) for k in {5120, 6144, 17408}}
+    ys = {n: torch.empty(1, n, device=dev) for n in {10240, 6144, 48, 5120, 12288, 1024, 17408}}
+    ya, yb, yv = torch.empty(1, 48, device=dev), torch.empty(1, 17408, device=dev), torch.empty(1, 1024, device=dev)
+
+    def token(_i):
+        idn = igq = 0
+        for li in range(layers):
+            if wl.model_layer_is_gqa(li):
+                q_, k_, v_, o_ = (gq[j][igq] for j in range(4))
+                q.gemv(q_, xs[5120], ys[12288], m=1)
+                q.gemv(k_, xs[5120], ys[1024], m=1)
+                q.gemv(v_, xs[5120], yv, m=1)
+                q.gemv(o_, xs[6144], ys[5120], m=1)
+                igq += 1
+            else:
+                a, z, ia, ib, out = (dn[j][idn] for j in range(5))
+                q.matmul_multi([a, z, ia, ib], xs[5120], [ys[10240], ys[6144], ys[48], ya], m=1)
+                q.gemv(out, xs[6144], ys[5120], m=1)
+                idn += 1
+            L = stack[li % len(stack)]
+            q.matmul_multi([L[2], L[3]], xs[5120], [ys[17408], yb], m=1)
+            q.gemv(L[4], xs[17408], ys[5120], m=1)
+    el, g = time_graph(torch, token, reps, 1, use_graph)
+    del g
+    tok_bytes = 0
+    for li in range(layers):
+        shapes = wl.MODEL_GQA_SHAPES if wl.model_layer_is_gqa(li) else wl.MODEL_DELTANET_SHAPES
+        tok_bytes += sum(wl.algorithmic_bytes(1, k, n) for _, k, n in shapes + wl.MODEL_MLP_SHAPES)
+    for pool in dn + gq:
+        for w in pool:
+            w.free()
+    n_launch = sum(4 if wl.model_layer_is_gqa(i) else 2 for i in range(layers)) + 2 * layers
+    return {"layers": layers, "deltanet_layers": n_dn, "gqa_layers": layers - n_dn,
+            "launches_per_token": n_launch, "bytes_per_token": tok_bytes,
+            "ms_per_token": round(el / reps * 1e3, 4), "GBps": round(tok_bytes * reps / el / 1e9, 1),
+            "frac_of_hbm_peak": round(tok_bytes * reps / el / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_host_abi(q, wl, calls=200):
+    """Per-call time of the drop-in q35_mm_fp8 (host x in, host y out,
+    synchronous) at configuration 0's and the qkv projection's shape,
+    through ctypes, on an already resident weight."""
+    import numpy as np
+    out = {}
+    for name, k, n, seed in (("single_5120x5120", 5120, 5120, wl.SEED_BASE + 0),
+                             ("qkv_5120x6144", 5120, 6144, wl.SEED_BASE + 1)):
+        W, sc = wl.gen_weight(seed, n, k)
+        x = wl.gen_act(seed + 0x100, 1, k)[0]
+        y = np.empty(n, np.float32)
+        args = (q._p(W, q._u8p), q._p(sc, q._u16p), n, k, q._p(x, q._f32p), q._p(y, q._f32p))
+        fn = q.lib.q35_mm_fp8
+        for _ in range(20):
+            fn(*args)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn(*args)
+        us = (time.perf_counter() - t0) / calls * 1e6
+        out[name] = {"us_per_call": round(us, 2), "calls": calls}
+        q.release(W)
+    out["note"] = ("q35_mm_fp8 on host pointers, weight already resident: fingerprint check, x copied in, "
+                   "GEMV, y copied out, stream synchronised; includes the ctypes call")
+    return out
 
 
 def bench_upload(q, wl, base, reps: int = 3):
@@ -318,6 +501,14 @@ def main():
                     help="skip the BF16 lm_head matvec (248320 x 5120)")
     ap.add_argument("--stack-layers", type=int, default=64,
                     help="distinct layers of the full-token weight stream (0: skip)")
+    ap.add_argument("--no-single", dest="single", action="store_false",
+                    help="skip configuration 0 (one 5120 x 5120 GEMV over a >= 1 GB pool of copies)")
+    ap.add_argument("--no-model-token", dest="model_token", action="store_false",
+                    help="skip the reference model's decode token (288 calls in its order)")
+    ap.add_argument("--no-host-abi", dest="host_abi", action="store_false",
+                    help="skip the per-call time of the drop-in q35_mm_fp8 on host pointers")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU time per CPU-baseline measurement")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="first run one plain device-to-device copy of MIB MiB (a known-size reference "
                          "kernel for hardware byte counters)")
@@ -349,7 +540,7 @@ def main():
         log(f"calibration copy: {args.calib_copy} MiB read + {args.calib_copy} MiB written")
         del src, dst
 
-    steps = max(args.pool, (args.steps + args.pool - 1) // args.pool * args.pool)
+    steps = max(1, args.steps)   # step i runs layer copy i % pool
     t = time.time()
     n_lay = max(args.pool, args.stack_layers)
     base, stack = make_layer_pool(q, wl, n_lay)
@@ -422,6 +613,26 @@ def main():
                      "frac_of_hbm_peak": round(tok_bytes * reps / el_s / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"stack: {stack_out}")
         del gs
+
+    # ---- configuration 0: one 5120 x 5120 GEMV over a >= 1 GB pool ----
+    single = None
+    if args.single:
+        single = bench_single(q, wl, torch, dev, max(steps, 64), args.warmup, not args.eager)
+        log(f"single: {single}")
+
+    # ---- the reference model's decode token: 288 calls in its order ----
+    model_token = None
+    if args.model_token and args.stack_layers:
+        model_token = bench_model_token(q, wl, torch, dev, stack, not args.eager)
+        log(f"model token: {model_token}")
+
+    # ---- the drop-in ABI on host pointers: per-call time ----
+    host_abi = None
+    if args.host_abi:
+        host_abi = bench_host_abi(q, wl)
+        if single:
+            host_abi["single_5120x5120"]["device_kernel_us"] = single["us"]
+        log(f"host abi: {host_abi}")
 
     # ---- MLP block at M = 1: RMSNorm -> gate/up -> SwiGLU -> down -> residual ----
     mlp_out = None
@@ -538,9 +749,15 @@ def main():
         tot_us = sum(v["us"] for v in prefill.values())
         tf_all = tot_flops / (tot_us * 1e-6) / 1e12
         prefill["total"] = {"TFLOPs": round(tf_all, 1), "frac_of_bf16_peak": round(tf_all / BF16_PEAK_TFLOPS, 4),
+                            "us": round(tot_us, 1),
                             "note": "includes the fp32->bf16 activation prepass kernel of each call; "
                                     "hipblaslt_bf16_TFLOPs = torch.mm of bf16 operands of the same shape "
                                     "(bf16 output), for context"}
+        prefill["roofline"] = {"bound": "mfma", "achieved": round(tf_all, 1), "peak": BF16_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(tf_all / BF16_PEAK_TFLOPS, 4),
+                               "kernel": "gemm_fp8_kernel (+ act_to_bf16_kernel, gemm_tail_kernel / "
+                                         "gemm_reduce_kernel)",
+                               "flops_per_call": {name: wl.flops(512, k, n) for name, k, n in wl.PREFILL_SHAPES}}
 
     # ---- BF16 lm_head matvec (q35_mm_bf16): 248320 x 5120 ----
     lm_head = None
@@ -577,7 +794,33 @@ def main():
         upload = bench_upload(q, wl, base)
         log(f"upload: {upload}")
 
-    cpu = None if args.no_cpu else cpu_baseline(wl, base)
+    cpu = None
+    cpu_run = None if args.no_cpu else cpu_baseline(args.cpu_budget)
+    if cpu_run:
+        host = cpu_run["host"]
+        hdesc = (f"{host.get('model')}, {host.get('sockets')} socket(s) x {host.get('cores_per_socket')} cores x "
+                 f"{host.get('threads_per_core')} threads, {host.get('numa_nodes')} NUMA node(s)")
+        cpu = {"value": cpu_run["layer"]["GBps"], "unit": "GB/s", "cores": cpu_run["threads"],
+               "kind": cpu_run["kind"],
+               "sample": f"{cpu_run['layer']['passes']} passes of one layer's 5 projections at M=1 (gate+up via "
+                         f"multi4), {cpu_run['layer']['bytes'] / 1e6:.1f} MB each, median "
+                         f"{cpu_run['layer']['ms']} ms/pass; "
+                         + ("oracle/_ref = the reference's q35_mm.c" if cpu_run["kind"] == "reference"
+                            else "oracle port") +
+                         f", OMP_NUM_THREADS={cpu_run['threads']} OMP_PROC_BIND={cpu_run['omp_proc_bind']} "
+                         f"OMP_PLACES={cpu_run['omp_places']} in a child process; host: {hdesc}",
+               "host": host, "threads": cpu_run["threads"], "omp_proc_bind": cpu_run["omp_proc_bind"],
+               "reference_auto_threads": cpu_run.get("reference_auto_threads")}
+        if single:
+            single["cpu_baseline"] = {"value": cpu_run["single"]["GBps"], "unit": "GB/s",
+                                      "ms": cpu_run["single"]["ms"], "cores": cpu_run["threads"],
+                                      "kind": cpu_run["kind"]}
+        if prefill:
+            ps = cpu_run["prefill_sample"]
+            prefill["cpu_baseline"] = {"value": ps["TFLOPs"], "unit": "TFLOP/s", "cores": cpu_run["threads"],
+                                       "kind": cpu_run["kind"],
+                                       "sample": f"first {ps['tokens']} of the 512 tokens of both shapes, "
+                                                 f"{ps}"}
 
     out = {
         "metric": METRIC,
@@ -600,6 +843,9 @@ def main():
         "cpu_baseline": cpu,
         "decode_sweep": sweep or None,
         "decode_stack": stack_out,
+        "single": single,
+        "decode_model_token": model_token,
+        "host_abi": host_abi,
         "prefill": prefill,
         "lm_head_bf16": lm_head,
         "mlp_block": mlp_out,
@@ -610,4 +856,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 2 and sys.argv[1] == CPU_CHILD:
+        cpu_child(float(sys.argv[2]))
+    else:
+        main()

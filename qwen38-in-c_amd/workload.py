@@ -32,6 +32,23 @@ DECODE_SHAPES = [  # (name, K, N)
     ("down", 17408, 5120),
 ]
 PREFILL_SHAPES = [("gate_up", 5120, 34816), ("down", 17408, 5120)]
+SINGLE_SHAPE = ("single", 5120, 5120)
+
+# The reference model's decode calls per layer besides the MLP (K, N):
+# a Gated DeltaNet layer makes one q35_mm_fp8_multi4 over in_proj_qkv /
+# in_proj_z / in_proj_a / in_proj_b (qwen35-c/src/q35_deltanet.c:325-329)
+# and one q35_mm_fp8 for out_proj (:360); a GQA layer three q35_mm_fp8 for
+# q / k / v (qwen35-c/src/q35_attn.c:273-275) and one for o_proj (:262).
+# Every layer then runs the MLP: one multi4 over gate and up, one call for
+# down (qwen35-c/src/q35_model.c:929-937).  Layers 3, 7, ..., 63 are GQA.
+MODEL_DELTANET_SHAPES = [("in_proj_qkv", 5120, 10240), ("in_proj_z", 5120, 6144), ("in_proj_a", 5120, 48),
+                         ("in_proj_b", 5120, 48), ("out_proj", 6144, 5120)]
+MODEL_GQA_SHAPES = [("q_proj", 5120, 12288), ("k_proj", 5120, 1024), ("v_proj", 5120, 1024), ("o_proj", 6144, 5120)]
+MODEL_MLP_SHAPES = [("gate_proj", 5120, 17408), ("up_proj", 5120, 17408), ("down_proj", 17408, 5120)]
+
+
+def model_layer_is_gqa(i: int) -> bool:
+    return i % 4 == 3
 STACK_LAYERS = 64          # 48 Gated DeltaNet + 16 GQA layers
 RAGGED = dict(m=37, k=4736, n=3000)
 

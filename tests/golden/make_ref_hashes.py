@@ -40,6 +40,20 @@ def cases():
     out.append(("edge_m3_129x129", 3, 129, 129, "normal", {}, b + 6))
     out.append(("tiny_m1_5x3", 1, 5, 3, "normal", {}, b + 7))
     out.append(("small_n48_m1_5120x48", 1, 5120, 48, "normal", {}, b + 8))
+    # The reference's decode projections besides the MLP: DeltaNet in_proj_qkv
+    # and in_proj_z (its multi4, qwen35-c/src/q35_deltanet.c:325-329; the 48-row
+    # in_proj_a/b are small_n48 above), GQA q and k/v
+    # (qwen35-c/src/q35_attn.c:273-275), out_proj / o_proj 6144 -> 5120
+    # (qwen35-c/src/q35_deltanet.c:360, qwen35-c/src/q35_attn.c:262).
+    for i, (nm, k, n) in enumerate((("dn_qkv", 5120, 10240), ("dn_z", 5120, 6144), ("attn_q", 5120, 12288),
+                                    ("attn_kv", 5120, 1024), ("out_proj", 6144, 5120))):
+        out.append((f"model_{nm}_m1_{k}x{n}", 1, k, n, "normal", {}, b + 0x20 + i))
+    # out_proj / o_proj over a prefill's tokens as one batch instead of the
+    # reference's per-token calls (qwen35-c/src/q35_deltanet.c:498,
+    # qwen35-c/src/q35_attn.c:262,311): 63 tokens (decode GEMV) and 512
+    # (prefill GEMM); activations plain fp32, as those callers pass them.
+    out.append(("straggler_m63_6144x5120", 63, 6144, 5120, "normal", {}, b + 0x30))
+    out.append(("straggler_m512_6144x5120", 512, 6144, 5120, "normal", {}, b + 0x31))
     return out
 
 
