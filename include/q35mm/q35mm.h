@@ -17,9 +17,11 @@
  * q35mm_last_error() describes the last failure of the calling thread.
  * Streams are hipStream_t passed as void*; NULL is HIP's null stream.
  *
- * Concurrency: the library keeps one split-K workspace per device.  Calls
- * whose kernels may overlap on the GPU (different streams without ordering)
- * race on it; serialise them on one stream.
+ * Concurrency: scratch memory between a call's kernels (split-K partials
+ * and counters, the GEMM's bf16 activations, the MLP block's intermediates)
+ * is kept per stream, so calls on different streams may overlap on the GPU.
+ * Calls on one stream run in order.  Host threads may call concurrently
+ * (calls are serialised on a library lock while they queue work).
  */
 #ifndef Q35MM_H
 #define Q35MM_H

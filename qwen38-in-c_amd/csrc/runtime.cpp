@@ -75,14 +75,22 @@ struct DevBuf {
     size_t cap = 0;
 };
 
-struct Device {
-    int id = -1;
-    hipStream_t stream = nullptr;
+// Scratch a launch sequence uses between its kernels.  One set per stream:
+// work queued on different streams may run concurrently, and a shared set
+// would let one call's kernels overwrite another's partials, counters or
+// staged activations.
+struct Scratch {
     DevBuf ws;        // split-K partials (float)
     DevBuf cnt;       // arrival counters (uint32, zero between launches)
     DevBuf xb;        // bf16 lane-order activations for the GEMM
-    DevBuf dx, dy;    // activation staging for the host-pointer ABI
     DevBuf mlp;       // MLP block intermediates (xn, gate, up, y)
+};
+
+struct Device {
+    int id = -1;
+    hipStream_t stream = nullptr;
+    std::unordered_map<hipStream_t, Scratch> scratch;
+    DevBuf dx, dy;    // activation staging for the host-pointer ABI
     void *up_pin[4] = {};        // pinned chunks of the file -> HBM upload ring
     void *up_dev[4] = {};        // device side of each chunk (+ room for its codes)
     hipEvent_t up_ev[4] = {};
@@ -92,6 +100,7 @@ struct Device {
     uint32_t cus = 256;
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
+    bool verify_full = false;   // Q35MM_VERIFY_WEIGHTS=full: fingerprint every byte of a reused host weight
     bool mlp_unfused = false;   // Q35MM_MLP_UNFUSED=1: separate neighbour kernels on the GEMV path
     bool gemv_rows = true;      // Q35MM_GEMV_ROWSPLIT=0: every weight on the stream-K GEMV
     uint32_t rows_depth = 0;    // Q35MM_ROWS_DEPTH: ring depth of the row-split GEMV (0: by launch)
@@ -118,6 +127,10 @@ int ensure_device() {
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
+    {
+        const char *v = getenv("Q35MM_VERIFY_WEIGHTS");
+        g_dev.verify_full = v && strcmp(v, "full") == 0;
+    }
     g_dev.mlp_unfused = env_u32("Q35MM_MLP_UNFUSED", 0) != 0;
     g_dev.cus = (uint32_t)prop.multiProcessorCount;
     g_dev.gemv_per_cu = std::max(1u, env_u32("Q35MM_GEMV_CTAS_PER_CU", kGemvCtasPerCu));
@@ -129,6 +142,8 @@ int ensure_device() {
 
 // Device-API streams follow the HIP convention: NULL is the null stream.
 hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
+
+Scratch &scratch_for(hipStream_t st) { return g_dev.scratch[st]; }
 
 // Grows a device buffer; waits for the device first because kernels queued
 // on any stream may still use the old allocation.
@@ -352,12 +367,13 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     }
     p.nctas = cta;
     p.max_range = max_range;
-    int rc = grow(g_dev.ws, (size_t)wsoff * sizeof(float), false);
+    Scratch &sc = scratch_for(st);
+    int rc = grow(sc.ws, (size_t)wsoff * sizeof(float), false);
     if (rc) return rc;
-    rc = grow(g_dev.cnt, (size_t)cntoff * sizeof(uint32_t), true);
+    rc = grow(sc.cnt, (size_t)cntoff * sizeof(uint32_t), true);
     if (rc) return rc;
-    p.ws = (float *)g_dev.ws.ptr;
-    p.cnt = (uint32_t *)g_dev.cnt.ptr;
+    p.ws = (float *)sc.ws.ptr;
+    p.cnt = (uint32_t *)sc.cnt.ptr;
     HIP_TRY(launch_gemv(p, st));
     return Q35MM_OK;
 }
@@ -414,10 +430,11 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     }
     const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus);
     const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w0.kb * kBlock * sizeof(uint16_t);
-    int rc = grow(g_dev.xb, xb_bytes, false);
+    Scratch &scr = scratch_for(st);
+    int rc = grow(scr.xb, xb_bytes, false);
     if (rc) return rc;
     if (pl.ws_bytes()) {
-        rc = grow(g_dev.ws, pl.ws_bytes(), false);
+        rc = grow(scr.ws, pl.ws_bytes(), false);
         if (rc) return rc;
     }
     GemmParams p{};
@@ -436,8 +453,8 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         tile0 += pl.mtiles * ((w.nb + 1) / 2);
     }
     p.nseg = nseg;
-    p.xb = (const uint16_t *)g_dev.xb.ptr;
-    p.ws = (float *)g_dev.ws.ptr;
+    p.xb = (const uint16_t *)scr.xb.ptr;
+    p.ws = (float *)scr.ws.ptr;
     p.m = m;
     p.kb = w0.kb;
     p.mtiles = pl.mtiles;
@@ -446,7 +463,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
     HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
-                               (uint16_t *)g_dev.xb.ptr, st));
+                               (uint16_t *)scr.xb.ptr, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -640,29 +657,40 @@ uint64_t mix64(uint64_t h, uint64_t v) {
     return h ^ (h >> 33);
 }
 
+// Four interleaved lanes: the multiply chains of a single running hash,
+// not the memory reads, were the cost (one chain over ~15 KB took ~3.5 us of
+// a host-pointer call).
 uint64_t hash_bytes(uint64_t h, const void *p, size_t n) {
     const uint8_t *b = (const uint8_t *)p;
+    uint64_t l[4] = {h, h ^ 0x243f6a8885a308d3ull, h ^ 0x13198a2e03707344ull, h ^ 0xa4093822299f31d0ull};
     size_t i = 0;
+    for (; i + 32 <= n; i += 32) {
+        uint64_t v[4];
+        memcpy(v, b + i, 32);
+        for (int j = 0; j < 4; j++) l[j] = mix64(l[j], v[j]);
+    }
     for (; i + 8 <= n; i += 8) {
         uint64_t v;
         memcpy(&v, b + i, 8);
-        h = mix64(h, v);
+        l[0] = mix64(l[0], v);
     }
     uint64_t tail = 0;
     for (; i < n; i++) tail = (tail << 8) | b[i];
-    return mix64(h, tail ^ n);
+    return mix64(mix64(mix64(mix64(l[0], l[1]), l[2]), l[3]), tail ^ n);
 }
 
-// Sampled fingerprint of a host weight: all scales, the first and last 4 KiB
-// of the codes and kFpWindows evenly spaced 256-byte windows.  It runs on
-// every host-pointer call; its cost is the memory latency of the scattered
-// windows (64 of them measured ~7 us of a ~48 us call), and a different
-// tensor behind a reused pointer differs almost everywhere, so a few windows
-// besides the scales and the edges suffice.
+// Fingerprint of a host weight, checked on every host-pointer call that
+// reuses a pointer: all scales, the first and last 4 KiB of the codes and
+// kFpWindows evenly spaced 256-byte windows.  A different tensor behind a
+// reused pointer differs almost everywhere, so a few windows besides the
+// scales and the edges suffice; an in-place edit of a few codes outside
+// them is not seen -- such callers call q35mm_release(W) after editing, or
+// set Q35MM_VERIFY_WEIGHTS=full, which hashes every byte on every call.
 constexpr size_t kFpWindows = 16;
 uint64_t fingerprint(const void *W, size_t wbytes, const void *sc, size_t scbytes) {
     uint64_t h = hash_bytes(0x51E5ull, sc, scbytes);
     const uint8_t *b = (const uint8_t *)W;
+    if (g_dev.verify_full) return hash_bytes(h, b, wbytes);
     const size_t edge = std::min<size_t>(4096, wbytes);
     h = hash_bytes(h, b, edge);
     h = hash_bytes(h, b + wbytes - edge, edge);
@@ -761,29 +789,44 @@ int resident_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, uint16_t **ou
 
 // Host-pointer round trip: X (n*cols floats) in, outputs of nseg segments
 // out.  'run' launches on g_dev.stream reading dx and writing dy[s].
+// Each queued DMA transfer costs ~8 us of latency (measured: H2D + GEMV +
+// D2H + synchronize 32 us against 17 us for the GEMV launch alone), so small
+// transfers skip the DMA engines: activations up to kDirectBytes are staged
+// in pinned memory and copied into HBM by a one-workgroup kernel, and
+// outputs up to kDirectBytes are written by the matmul kernels straight
+// into pinned (device-visible) host memory.
+constexpr size_t kDirectBytes = 256 * 1024;
+
 template <class Run>
 int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t *yfloats,
                    uint32_t nseg, Run run) {
     size_t ytotal = 0;
     for (uint32_t s = 0; s < nseg; s++) ytotal += yfloats[s];
+    const bool direct_x = xfloats * sizeof(float) <= kDirectBytes;
+    const bool direct_y = ytotal * sizeof(float) <= kDirectBytes;
     int rc = grow(g_dev.dx, xfloats * sizeof(float), false);
-    if (!rc) rc = grow(g_dev.dy, ytotal * sizeof(float), false);
-    if (!rc) rc = grow_pinned((xfloats + ytotal) * sizeof(float));
+    if (!rc && !direct_y) rc = grow(g_dev.dy, ytotal * sizeof(float), false);
+    // x and y regions of the pinned buffer each start 256-byte aligned
+    const size_t xpad = (xfloats + 63) & ~(size_t)63;
+    if (!rc) rc = grow_pinned((xpad + ytotal) * sizeof(float));
     if (rc) return rc;
     float *px = (float *)g_dev.pin;
-    float *py = px + xfloats;
+    float *py = px + xpad;
     hipStream_t st = g_dev.stream;
     memcpy(px, X, xfloats * sizeof(float));
-    HIP_TRY(hipMemcpyAsync(g_dev.dx.ptr, px, xfloats * sizeof(float), hipMemcpyHostToDevice, st));
+    if (direct_x)
+        HIP_TRY(launch_copy_f32(px, (float *)g_dev.dx.ptr, xfloats, st));
+    else
+        HIP_TRY(hipMemcpyAsync(g_dev.dx.ptr, px, xfloats * sizeof(float), hipMemcpyHostToDevice, st));
     float *dys[4];
     size_t off = 0;
     for (uint32_t s = 0; s < nseg; s++) {
-        dys[s] = (float *)g_dev.dy.ptr + off;
+        dys[s] = (direct_y ? py : (float *)g_dev.dy.ptr) + off;
         off += yfloats[s];
     }
     rc = run((const float *)g_dev.dx.ptr, dys);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (!direct_y) HIP_TRY(hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
     off = 0;
     for (uint32_t s = 0; s < nseg; s++) {
@@ -907,8 +950,24 @@ Q35MM_API void q35_mm_fp8_multi4(const uint8_t *W[4], const uint16_t *sc[4], uin
     }
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     int rc = ensure_device();
-    q35mm_weight *ws[4];
-    for (uint32_t i = 0; i < nseg && !rc; i++) rc = resident_fp8(W[idx[i]], sc[idx[i]], rows[idx[i]], cols, &ws[i]);
+    // A pointer repeated with another row count or scale pointer gets a copy
+    // of its own for this call: the registry holds one copy per pointer, and
+    // replacing it would free an earlier segment's copy while the launch
+    // still needs it.
+    q35mm_weight *ws[4], *tmp[4] = {};
+    for (uint32_t i = 0; i < nseg && !rc; i++) {
+        const uint32_t s = idx[i];
+        bool clash = false;
+        for (uint32_t j = 0; j < i; j++)
+            clash |= W[idx[j]] == W[s] && (rows[idx[j]] != rows[s] || sc[idx[j]] != sc[s]);
+        if (clash) {
+            const std::vector<float> f = widen_scales(sc[s], rows[s], cols);
+            rc = weight_create(W[s], f.data(), rows[s], cols, &tmp[i]);
+            ws[i] = tmp[i];
+        } else {
+            rc = resident_fp8(W[s], sc[s], rows[s], cols, &ws[i]);
+        }
+    }
     if (!rc) {
         float *ys[4];
         size_t yf[4];
@@ -920,6 +979,8 @@ Q35MM_API void q35_mm_fp8_multi4(const uint8_t *W[4], const uint16_t *sc[4], uin
             return run_gemv(ws, nseg, 1, dx, dy, g_dev.stream);
         });
     }
+    for (uint32_t i = 0; i < nseg; i++)
+        if (tmp[i]) q35mm_weight_destroy(tmp[i]);
     if (rc) die("q35_mm_fp8_multi4");
 }
 
@@ -1108,10 +1169,11 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
     if (!dX || !dNormW) return set_error(Q35MM_EINVAL, "null pointer");
     // workspace: xn [m][H], g [m][I], u [m][I], y [m][H]; SwiGLU writes g in place
     const size_t nh = (size_t)m * H, ni = (size_t)m * I;
-    rc = grow(g_dev.mlp, (2 * nh + 2 * ni) * sizeof(float), false);
-    if (rc) return rc;
-    float *xn = (float *)g_dev.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     hipStream_t st = pick_stream(stream);
+    Scratch &scr = scratch_for(st);
+    rc = grow(scr.mlp, (2 * nh + 2 * ni) * sizeof(float), false);
+    if (rc) return rc;
+    float *xn = (float *)scr.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     const bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(gate->w, m) &&
                       gemm_fits(up->w, m) && gemm_fits(down->w, m);
     if (!gemm) {
@@ -1292,7 +1354,11 @@ Q35MM_API void q35mm_shutdown(void) {
     q35mm_release_all();
     if (g_dev.id < 0) return;
     (void)hipDeviceSynchronize();
-    for (DevBuf *b : {&g_dev.ws, &g_dev.cnt, &g_dev.xb, &g_dev.dx, &g_dev.dy, &g_dev.mlp}) {
+    for (auto &kv : g_dev.scratch)
+        for (DevBuf *b : {&kv.second.ws, &kv.second.cnt, &kv.second.xb, &kv.second.mlp})
+            if (b->ptr) (void)hipFree(b->ptr);
+    g_dev.scratch.clear();
+    for (DevBuf *b : {&g_dev.dx, &g_dev.dy}) {
         if (b->ptr) (void)hipFree(b->ptr);
         b->ptr = nullptr;
         b->cap = 0;

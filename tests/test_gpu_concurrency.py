@@ -1,0 +1,139 @@
+"""Concurrency and residency edge cases of libq35mm.so on the GPU.
+
+- Calls on two streams that overlap on the GPU: each stream has its own
+  scratch (stream-K split partials and counters, the GEMM's bf16
+  activations), so both results equal the oracle's and the single-stream
+  bits.
+- A q35_mm_fp8_multi4 that passes one weight pointer twice with different
+  row counts (the reference reads the same bytes both ways,
+  qwen35-c/src/q35_mm.c:176-198).
+- The host-pointer residency check: a new tensor behind a reused pointer is
+  seen; an in-place edit of a few codes outside the sampled fingerprint is
+  not, until q35mm_release(W), or always with Q35MM_VERIFY_WEIGHTS=full.
+
+Bars: decode GEMV ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5; prefill GEMM
+rel-L2 <= 5e-3 and max-abs <= 2e-2; bitwise where results must equal
+other calls of the library.
+"""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-5
+
+
+def _dev(a, gpu):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(gpu)
+
+
+def test_two_streams_overlap(q, oracle, wl, gpu):
+    """Stream-K GEMVs (K of 168 blocks, beyond the row-split kernel) and
+    prefill GEMMs queued alternately on two streams, 20 rounds without
+    synchronising in between; every output equals the same call made alone."""
+    import torch
+    k = 168 * 128
+    Wa, sa = wl.gen_weight(301, 1500, k)
+    Wb, sb = wl.gen_weight(302, 900, k)
+    Wg, sg_ = wl.gen_weight(303, 700, 2048)
+    wa, wb, wg = q.Weight(Wa, sa), q.Weight(Wb, sb), q.Weight(Wg, sg_)
+    xa, xb = _dev(wl.gen_act(304, 3, k), gpu), _dev(wl.gen_act(305, 5, k), gpu)
+    Xg1, Xg2 = _dev(wl.gen_act(306, 96, 2048), gpu), _dev(wl.gen_act(307, 160, 2048), gpu)
+    ref = {}
+    for name, w, x, m, gemm in (("a", wa, xa, 3, False), ("b", wb, xb, 5, False),
+                                ("g1", wg, Xg1, 96, True), ("g2", wg, Xg2, 160, True)):
+        y = torch.empty((m, w.rows), device=gpu)
+        (q.gemm if gemm else q.gemv)(w, x, y)
+        torch.cuda.synchronize()
+        ref[name] = y.cpu().numpy()
+    ya = oracle.mm_batch(Wa, sa, xa.cpu().numpy())
+    for t in range(3):
+        assert normwise_rel(ref["a"][t], ya[t]) <= GEMV_TOL
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for r in range(20):
+        with torch.cuda.stream(s1):
+            y1 = torch.empty((3, wa.rows), device=gpu)
+            g1 = torch.empty((96, wg.rows), device=gpu)
+            q.gemv(wa, xa, y1)
+            q.gemm(wg, Xg1, g1)
+        with torch.cuda.stream(s2):
+            y2 = torch.empty((5, wb.rows), device=gpu)
+            g2 = torch.empty((160, wg.rows), device=gpu)
+            q.gemv(wb, xb, y2)
+            q.gemm(wg, Xg2, g2)
+        outs.append((y1, g1, y2, g2))
+    torch.cuda.synchronize()
+    for y1, g1, y2, g2 in outs:
+        for got, name in ((y1, "a"), (g1, "g1"), (y2, "b"), (g2, "g2")):
+            assert (got.cpu().numpy().view(np.uint32) == ref[name].view(np.uint32)).all(), name
+    for w in (wa, wb, wg):
+        w.free()
+
+
+def test_multi4_repeated_pointer_other_rows(q, oracle, wl, gpu):
+    """W and its first 128 rows (same pointer) in one multi4 call, twice, and
+    then single calls: each segment as its single call, bit for bit."""
+    W, sc = wl.gen_weight(311, 384, 1024)
+    x = wl.gen_act(312, 1, 1024)[0]
+    head = W[:128]
+    assert head.ctypes.data == W.ctypes.data
+    for _ in range(2):
+        y_full, y_head = q.mm_fp8_multi4([W, head], [sc, sc[:1]], x)[:2]
+        assert normwise_rel(y_full, oracle.mm(W, sc, x)) <= GEMV_TOL
+        assert normwise_rel(y_head, oracle.mm(head, sc[:1], x)) <= GEMV_TOL
+    assert (q.mm_fp8(W, sc, x).view(np.uint32) == y_full.view(np.uint32)).all()
+    q.release(W)
+    assert (q.mm_fp8(head, sc[:1], x).view(np.uint32) == y_head.view(np.uint32)).all()
+    q.release(W)
+
+
+def test_in_place_edit_needs_release(q, oracle, wl, gpu):
+    """An edit of a few codes between the fingerprint's sampled windows keeps
+    the resident copy (the documented limit); q35mm_release(W) picks it up."""
+    W, sc = wl.gen_weight(321, 512, 4096)
+    x = wl.gen_act(322, 1, 4096)[0]
+    y0 = q.mm_fp8(W, sc, x)
+    # row 300, columns 1000..1007: offset 1229800, inside no 256-byte window
+    # (windows start every (2097152 - 256) / 15 = 139793 bytes) nor the edges
+    off = 300 * 4096 + 1000
+    assert all(not (o <= off < o + 256) for o in [(W.size - 256) // 15 * i for i in range(16)])
+    W[300, 1000:1008] ^= np.uint8(0x80)
+    y_stale = q.mm_fp8(W, sc, x)
+    assert (y_stale.view(np.uint32) == y0.view(np.uint32)).all()
+    q.release(W)
+    y_new = q.mm_fp8(W, sc, x)
+    assert normwise_rel(y_new, oracle.mm(W, sc, x)) <= GEMV_TOL
+    assert not (y_new.view(np.uint32) == y0.view(np.uint32)).all()
+    q.release(W)
+
+
+def test_verify_weights_full_sees_in_place_edit():
+    """With Q35MM_VERIFY_WEIGHTS=full the same edit is seen without a release
+    (a fresh process: the setting is read when the library initialises)."""
+    code = r"""
+import sys, numpy as np
+sys.path.insert(0, %r); sys.path.insert(0, %r)
+import q35mm as q, workload as wl
+from oracle import Oracle
+W, sc = wl.gen_weight(321, 512, 4096)
+x = wl.gen_act(322, 1, 4096)[0]
+y0 = q.mm_fp8(W, sc, x)
+W[300, 1000:1008] ^= np.uint8(0x80)
+y1 = q.mm_fp8(W, sc, x)
+yr = Oracle().mm(W, sc, x)
+d = float(np.abs(y1.astype(np.float64) - yr).max() / np.abs(yr).max())
+print("changed", int(not (y1.view(np.uint32) == y0.view(np.uint32)).all()), "err", d)
+""" % (os.path.join(ROOT, "qwen38-in-c_amd"), os.path.join(ROOT, "oracle"))
+    env = dict(os.environ, Q35MM_VERIFY_WEIGHTS="full")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    words = out.stdout.split()
+    assert words[0] == "changed" and words[1] == "1" and float(words[3]) <= GEMV_TOL, out.stdout
