@@ -200,6 +200,17 @@ hipError_t launch_copy_f32(const float *src, float *dst, size_t n, hipStream_t s
 hipError_t launch_bf16_gemv(const uint16_t *w, uint32_t rows, uint32_t cols,
                             const float *x, float *y, hipStream_t stream);
 
+// ---- allocation-free scratch (noalloc.hip) -----------------------------
+// q35mm_matmul_noalloc's scratch: counters first (zero between launches),
+// then one region for split partials and staged activations.
+constexpr size_t kNoAllocCntBytes = 64u << 10;
+constexpr size_t kNoAllocBytes = 16u << 20;
+// Once per device, with the device current: resolve the scratch array's
+// address and clear its counters (synchronises stream).
+hipError_t noalloc_setup(int device, hipStream_t stream);
+// The device address of the array (nullptr before noalloc_setup).
+uint8_t *noalloc_scratch(int device);
+
 // ---- load-time quantizer (quantize.hip) --------------------------------
 // w [rows][cols] (fp32, or bf16 bits) -> row-major e4m3 codes and the
 // [ceil(rows/128)][ceil(cols/128)] block scales as bf16 bits and/or fp32

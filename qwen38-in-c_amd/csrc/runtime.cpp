@@ -84,6 +84,9 @@ struct Scratch {
     DevBuf cnt;       // arrival counters (uint32, zero between launches)
     DevBuf xb;        // bf16 lane-order activations for the GEMM
     DevBuf mlp;       // MLP block intermediates (xn, gate, up, y)
+    // Set for q35mm_matmul_noalloc: the device address of the fixed scratch
+    // array (noalloc.hip); nothing is allocated, oversized requests fail.
+    uint8_t *fixed = nullptr;
 };
 
 struct Device {
@@ -124,6 +127,7 @@ int ensure_device() {
                          prop.gcnArchName);
     HIP_TRY(hipSetDevice(dev));
     HIP_TRY(hipStreamCreateWithFlags(&g_dev.stream, hipStreamNonBlocking));
+    HIP_TRY(noalloc_setup(dev, g_dev.stream));
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
@@ -144,6 +148,7 @@ int ensure_device() {
 hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
 Scratch &scratch_for(hipStream_t st) { return g_dev.scratch[st]; }
+
 
 // Grows a device buffer; waits for the device first because kernels queued
 // on any stream may still use the old allocation.
@@ -176,6 +181,43 @@ int grow_pinned(size_t bytes) {
         return set_error(Q35MM_ENOMEM, "hipHostMalloc(%zu) failed", cap);
     }
     g_dev.pin_cap = cap;
+    return Q35MM_OK;
+}
+
+// Stream-K partials and arrival counters of one launch.
+int scratch_splitk(Scratch &s, size_t ws_bytes, size_t cnt_bytes, float **ws, uint32_t **cnt) {
+    if (s.fixed) {
+        if (cnt_bytes > kNoAllocCntBytes || ws_bytes > kNoAllocBytes)
+            return set_error(Q35MM_EINVAL, "no-alloc scratch: %zu bytes of partials and %zu of counters needed, "
+                             "%zu and %zu available", ws_bytes, cnt_bytes, kNoAllocBytes, kNoAllocCntBytes);
+        *cnt = reinterpret_cast<uint32_t *>(s.fixed);
+        *ws = reinterpret_cast<float *>(s.fixed + kNoAllocCntBytes);
+        return Q35MM_OK;
+    }
+    int rc = grow(s.ws, ws_bytes, false);
+    if (!rc) rc = grow(s.cnt, cnt_bytes, true);
+    if (rc) return rc;
+    *ws = (float *)s.ws.ptr;
+    *cnt = (uint32_t *)s.cnt.ptr;
+    return Q35MM_OK;
+}
+
+// The GEMM's lane-order bf16 activations and K-slice partials.
+int scratch_gemm(Scratch &s, size_t xb_bytes, size_t ws_bytes, uint16_t **xb, float **ws) {
+    if (s.fixed) {
+        const size_t xb_al = (xb_bytes + 255) & ~(size_t)255;
+        if (xb_al + ws_bytes > kNoAllocBytes)
+            return set_error(Q35MM_EINVAL, "no-alloc scratch: %zu bytes of activations and %zu of partials "
+                             "needed, %zu available", xb_bytes, ws_bytes, kNoAllocBytes);
+        *xb = reinterpret_cast<uint16_t *>(s.fixed + kNoAllocCntBytes);
+        *ws = reinterpret_cast<float *>(s.fixed + kNoAllocCntBytes + xb_al);
+        return Q35MM_OK;
+    }
+    int rc = grow(s.xb, xb_bytes, false);
+    if (!rc && ws_bytes) rc = grow(s.ws, ws_bytes, false);
+    if (rc) return rc;
+    *xb = (uint16_t *)s.xb.ptr;
+    *ws = (float *)s.ws.ptr;
     return Q35MM_OK;
 }
 
@@ -300,7 +342,7 @@ uint32_t gemv_kind(const Weight &w) {
 bool uses_gemv_rows(const Weight &w) { return gemv_kind(w) != kStreamK; }
 
 int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
-                   float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid) {
+                   float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid, Scratch *scr) {
     GemvParams p{};
     const uint32_t cols = w[0]->w.cols, KB = w[0]->w.kb;
     p.x = dX;
@@ -367,13 +409,9 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     }
     p.nctas = cta;
     p.max_range = max_range;
-    Scratch &sc = scratch_for(st);
-    int rc = grow(sc.ws, (size_t)wsoff * sizeof(float), false);
+    const int rc = scratch_splitk(scr ? *scr : scratch_for(st), (size_t)wsoff * sizeof(float),
+                                  (size_t)cntoff * sizeof(uint32_t), &p.ws, &p.cnt);
     if (rc) return rc;
-    rc = grow(sc.cnt, (size_t)cntoff * sizeof(uint32_t), true);
-    if (rc) return rc;
-    p.ws = (float *)sc.ws.ptr;
-    p.cnt = (uint32_t *)sc.cnt.ptr;
     HIP_TRY(launch_gemv(p, st));
     return Q35MM_OK;
 }
@@ -382,7 +420,7 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
 // launch, row-split weights another.
 int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
              float *const *dY, hipStream_t st, const GemvInput &in = GemvInput(),
-             float *const *resid = nullptr) {
+             float *const *resid = nullptr, Scratch *scr = nullptr) {
     const uint32_t cols = w[0]->w.cols;
     for (uint32_t t0 = 0; t0 < m; t0 += kGemvMaxM) {
         const uint32_t mg = std::min(kGemvMaxM, m - t0);
@@ -400,7 +438,7 @@ int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const floa
                 n++;
             }
             if (!n) continue;
-            int rc = run_gemv_group(wg, n, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr);
+            int rc = run_gemv_group(wg, n, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr, scr);
             if (rc) return rc;
         }
     }
@@ -419,7 +457,8 @@ bool gemm_fits(const Weight &w, uint32_t m) {
 // resid[s] (y = resid + product, may alias y) and x2 (the activations are
 // silu(x) * x2, formed while rounding them to bf16).
 int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const float *dX, float *const *dY,
-             hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr) {
+             hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr,
+             Scratch *scr = nullptr) {
     const Weight &w0 = wt[0]->w;
     uint32_t ntiles = 0;
     for (uint32_t s = 0; s < nseg; s++) {
@@ -430,13 +469,10 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     }
     const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus);
     const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w0.kb * kBlock * sizeof(uint16_t);
-    Scratch &scr = scratch_for(st);
-    int rc = grow(scr.xb, xb_bytes, false);
+    uint16_t *xb = nullptr;
+    float *ws = nullptr;
+    const int rc = scratch_gemm(scr ? *scr : scratch_for(st), xb_bytes, pl.ws_bytes(), &xb, &ws);
     if (rc) return rc;
-    if (pl.ws_bytes()) {
-        rc = grow(scr.ws, pl.ws_bytes(), false);
-        if (rc) return rc;
-    }
     GemmParams p{};
     uint32_t tile0 = 0;
     for (uint32_t s = 0; s < nseg; s++) {
@@ -453,8 +489,8 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         tile0 += pl.mtiles * ((w.nb + 1) / 2);
     }
     p.nseg = nseg;
-    p.xb = (const uint16_t *)scr.xb.ptr;
-    p.ws = (float *)scr.ws.ptr;
+    p.xb = xb;
+    p.ws = ws;
     p.m = m;
     p.kb = w0.kb;
     p.mtiles = pl.mtiles;
@@ -463,7 +499,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
     HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
-                               (uint16_t *)scr.xb.ptr, st));
+                               xb, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -473,12 +509,14 @@ int check_weight(const q35mm_weight *w) {
     return Q35MM_OK;
 }
 
-int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hipStream_t st) {
+int run_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, hipStream_t st,
+               Scratch *scr = nullptr) {
     if (m == 0) return Q35MM_OK;
     const q35mm_weight *ws[1] = {w};
     float *ys[1] = {dY};
-    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(w->w, m)) return run_gemm(ws, 1, m, dX, ys, st);
-    return run_gemv(ws, 1, m, dX, ys, st);
+    if (m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(w->w, m))
+        return run_gemm(ws, 1, m, dX, ys, st, nullptr, nullptr, scr);
+    return run_gemv(ws, 1, m, dX, ys, st, GemvInput(), nullptr, scr);
 }
 
 // ---------------------------------------------------------------------
@@ -1058,6 +1096,19 @@ Q35MM_API int q35mm_matmul(const q35mm_weight *w, uint32_t m, const float *dX, f
     if (rc) return rc;
     if (m && (!dX || !dY)) return set_error(Q35MM_EINVAL, "null activation pointer");
     return run_matmul(w, m, dX, dY, pick_stream(stream));
+}
+
+Q35MM_API int q35mm_matmul_noalloc(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (g_dev.id < 0)
+        return set_error(Q35MM_EINVAL, "q35mm_matmul_noalloc: library not initialised (call q35mm_init first)");
+    int rc = check_weight(w);
+    if (rc) return rc;
+    if (m && (!dX || !dY)) return set_error(Q35MM_EINVAL, "null activation pointer");
+    Scratch fixed;
+    fixed.fixed = noalloc_scratch(g_dev.id);
+    if (!fixed.fixed) return set_error(Q35MM_EINVAL, "q35mm_matmul_noalloc: no scratch on device %d", g_dev.id);
+    return run_matmul(w, m, dX, dY, pick_stream(stream), &fixed);
 }
 
 Q35MM_API int q35mm_gemv(const q35mm_weight *w, uint32_t m, const float *dX, float *dY, void *stream) {

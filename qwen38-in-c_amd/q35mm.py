@@ -74,7 +74,7 @@ def _load(path: str = LIB_PATH) -> C.CDLL:
     lib.q35mm_weight_shape.argtypes = [vp, _u32p, _u32p]
     lib.q35mm_weight_bytes.argtypes = [vp]
     lib.q35mm_weight_bytes.restype = C.c_size_t
-    for name in ("q35mm_matmul", "q35mm_gemv", "q35mm_gemm"):
+    for name in ("q35mm_matmul", "q35mm_gemv", "q35mm_gemm", "q35mm_matmul_noalloc"):
         getattr(lib, name).argtypes = [vp, C.c_uint32, vp, vp, vp]
     lib.q35mm_matmul_multi.argtypes = [C.POINTER(vp), C.c_uint32, C.c_uint32, vp, C.POINTER(vp), vp]
     lib.q35mm_dequant_f32.argtypes = [vp, vp, vp]
@@ -128,6 +128,11 @@ def _check(rc: int, what: str) -> None:
 # ---------------------------------------------------------------------------
 # Drop-in ABI (host pointers)
 # ---------------------------------------------------------------------------
+def init(device: int = -1) -> None:
+    """q35mm_init: select and initialise the device (-1: the default)."""
+    _check(lib.q35mm_init(device), "q35mm_init")
+
+
 def impl() -> str:
     return lib.q35_mm_impl_fp8().decode()
 
@@ -293,6 +298,12 @@ class Weight:
 def matmul(w: Weight, X, Y, m: int | None = None, stream=None) -> None:
     m = X.shape[0] if m is None else m
     _check(lib.q35mm_matmul(w.handle, m, _dptr(X), _dptr(Y), _stream(stream)), "q35mm_matmul")
+
+
+def matmul_noalloc(w: Weight, X, Y, m: int | None = None, stream=None) -> None:
+    """q35mm_matmul_noalloc: q35mm_matmul on the library's fixed scratch."""
+    m = X.shape[0] if m is None else m
+    _check(lib.q35mm_matmul_noalloc(w.handle, m, _dptr(X), _dptr(Y), _stream(stream)), "q35mm_matmul_noalloc")
 
 
 def gemv(w: Weight, X, Y, m: int | None = None, stream=None) -> None:
