@@ -93,6 +93,7 @@ struct Device {
     int id = -1;
     hipStream_t stream = nullptr;
     std::unordered_map<hipStream_t, Scratch> scratch;
+    Scratch *last_scratch = nullptr;   // of the most recent call outside graph capture
     DevBuf dx, dy;    // activation staging for the host-pointer ABI
     void *up_pin[4] = {};        // pinned chunks of the file -> HBM upload ring
     void *up_dev[4] = {};        // device side of each chunk (+ room for its codes)
@@ -147,7 +148,22 @@ int ensure_device() {
 // Device-API streams follow the HIP convention: NULL is the null stream.
 hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
-Scratch &scratch_for(hipStream_t st) { return g_dev.scratch[st]; }
+// The scratch of stream st.  A stream first seen while it is being captured
+// into a graph cannot allocate: it shares the scratch of the most recent
+// call made outside capture (its warm-up, in the usual capture pattern), so
+// such a graph and eager work on that stream must not run at the same time.
+Scratch &scratch_for(hipStream_t st) {
+    auto it = g_dev.scratch.find(st);
+    if (it == g_dev.scratch.end()) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (g_dev.last_scratch && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return *g_dev.last_scratch;
+        it = g_dev.scratch.emplace(st, Scratch()).first;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) g_dev.last_scratch = &it->second;
+    return it->second;
+}
 
 
 // Grows a device buffer; waits for the device first because kernels queued
@@ -1409,6 +1425,7 @@ Q35MM_API void q35mm_shutdown(void) {
         for (DevBuf *b : {&kv.second.ws, &kv.second.cnt, &kv.second.xb, &kv.second.mlp})
             if (b->ptr) (void)hipFree(b->ptr);
     g_dev.scratch.clear();
+    g_dev.last_scratch = nullptr;
     for (DevBuf *b : {&g_dev.dx, &g_dev.dy}) {
         if (b->ptr) (void)hipFree(b->ptr);
         b->ptr = nullptr;

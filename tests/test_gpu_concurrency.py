@@ -137,3 +137,35 @@ print("changed", int(not (y1.view(np.uint32) == y0.view(np.uint32)).all()), "err
     assert out.returncode == 0, out.stderr[-2000:]
     words = out.stdout.split()
     assert words[0] == "changed" and words[1] == "1" and float(words[3]) <= GEMV_TOL, out.stdout
+
+
+def test_graph_captured_on_a_fresh_stream(q, wl, gpu):
+    """Warm-up calls on one stream, capture on a stream the library has not
+    seen (the pattern of torch.cuda.graph's own capture stream): the capture
+    cannot allocate, so the stream borrows the warm-up's scratch; each
+    replay, with eager calls in between, gives the eager bits."""
+    import torch
+    W, sc = wl.gen_weight(331, 700, 2048)
+    w = q.Weight(W, sc)
+    X = _dev(wl.gen_act(332, 96, 2048), gpu)
+    want = torch.empty((96, 700), device=gpu)
+    q.gemm(w, X, want)                      # warm-up on the current stream
+    torch.cuda.synchronize()
+    Y = torch.empty_like(want)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            q.gemm(w, X, Y)
+    torch.cuda.synchronize()
+    other = torch.empty((64, 700), device=gpu)
+    for r in range(3):
+        Y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert (Y.cpu().numpy().view(np.uint32) == want.cpu().numpy().view(np.uint32)).all(), r
+        q.gemm(w, X[:64], other)
+        torch.cuda.synchronize()
+    del g
+    w.free()
