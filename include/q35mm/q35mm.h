@@ -92,7 +92,9 @@ int q35mm_gemv(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
 /* Prefill GEMM for any m: activations rounded to bf16, bf16 MFMA with fp32
  * accumulation, fp32 block scale applied per 128-wide K step.  The bf16
  * activations (m rounded up to 256 rows) and the resident weight must each
- * stay under 4 GiB (Q35MM_EINVAL otherwise; q35mm_matmul then uses the GEMV). */
+ * stay under 4 GiB, and the live block scales of every 128-row group must
+ * lie within a factor of 2^64 of each other (Q35MM_EINVAL otherwise;
+ * q35mm_matmul then uses the GEMV). */
 int q35mm_gemm(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
                void *stream);
 /* Up to four weights sharing cols and X, one launch (rows may differ);

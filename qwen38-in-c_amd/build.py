@@ -4,7 +4,9 @@
     python qwen38-in-c_amd/build.py --asm    # also dump device assembly to _build/
 
 The library is written to qwen38-in-c_amd/lib/libq35mm.so; tests, the
-benchmark and the smoke check load it from there.
+benchmark and the smoke check load it from there.  The ceiling probe
+(probes/q35mm_probe.hip: raw weight-read rate, MFMA issue rate) is built
+beside it as lib/q35mm_probe.
 """
 from __future__ import annotations
 
@@ -48,6 +50,25 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+PROBE_SRC = os.path.join(PKG, "probes", "q35mm_probe.hip")
+PROBE = os.path.join(LIBDIR, "q35mm_probe")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """The ceiling probe (raw weight reads, MFMA issue rate): a separate
+    executable, not part of the library."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = PROBE + ".tmp"
+    cmd = [HIPCC, *DEVICE_FLAGS, "-O3", "-std=c++17", "-o", tmp, PROBE_SRC]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed on the probe:\n" + res.stdout + res.stderr)
+    os.replace(tmp, PROBE)
+    return PROBE
+
+
 def dump_asm(outdir: str) -> None:
     os.makedirs(outdir, exist_ok=True)
     for src in glob.glob(os.path.join(CSRC, "*.hip")):
@@ -58,5 +79,6 @@ def dump_asm(outdir: str) -> None:
 
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    print(build_probe())
     if "--asm" in sys.argv:
         dump_asm(os.path.join(ROOT, "_build", "asm"))

@@ -21,7 +21,13 @@ struct Weight {
     float *scale = nullptr;     // [NB][KB] fp32 (padded blocks are 0)
     uint32_t rows = 0, cols = 0;
     uint32_t nb = 0, kb = 0;    // ceil(rows/128), ceil(cols/128)
+    // Live (nonzero) block scales of some 128-row group span more than
+    // kGemmScaleSpan: the prefill GEMM, which keeps its accumulator in units
+    // of the current block scale, could overflow, so such a weight runs on
+    // the decode GEMV (one fmaf per block and output) at any m.
+    bool wide_scales = false;
 };
+constexpr float kGemmScaleSpan = 0x1.0p64f;
 
 // ---- decode GEMV (m <= 8 tokens) -------------------------------------
 // Stream-K decomposition: the weight's NB*KB 16 KiB blocks, taken in

@@ -279,6 +279,23 @@ int weight_alloc_fill(uint32_t rows, uint32_t cols, q35mm_weight **out, Fill fil
     if (rc) return fail(rc);
     if (hipStreamSynchronize(st) != hipSuccess)
         return fail(set_error(Q35MM_EHIP, "weight upload failed: %s", hipGetErrorString(hipGetLastError())));
+    // the spread of live scales per row group, from the resident fp32 scales
+    // (whatever produced them: host arrays, a checkpoint, the device quantizer)
+    {
+        std::vector<float> sc((size_t)nb * kb);
+        if (hipMemcpy(sc.data(), h->w.scale, scale_bytes, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(set_error(Q35MM_EHIP, "scale read-back failed"));
+        for (uint32_t g = 0; g < nb && !h->w.wide_scales; g++) {
+            float lo = INFINITY, hi = 0.0f;
+            for (uint32_t j = 0; j < kb; j++) {
+                const float v = std::fabs(sc[(size_t)g * kb + j]);
+                if (v == 0.0f || v != v) continue;
+                lo = std::min(lo, v);
+                hi = std::max(hi, v);
+            }
+            h->w.wide_scales = hi > 0.0f && (std::isinf(hi) || hi / lo > kGemmScaleSpan);
+        }
+    }
     h->bytes = tiled_bytes + scale_bytes;
     *out = h;
     return Q35MM_OK;
@@ -463,6 +480,7 @@ int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const floa
 
 // The GEMM kernel addresses both operands with 32-bit byte offsets.
 bool gemm_fits(const Weight &w, uint32_t m) {
+    if (w.wide_scales) return false;
     const uint64_t mtiles = (m + kGemmTile - 1) / kGemmTile;
     const uint64_t xb_bytes = mtiles * kGemmTile * w.kb * kBlock * sizeof(uint16_t);
     const uint64_t w_bytes = (uint64_t)w.nb * w.kb * kBlockBytes;
@@ -479,6 +497,9 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     uint32_t ntiles = 0;
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &w = wt[s]->w;
+        if (w.wide_scales)
+            return set_error(Q35MM_EINVAL, "block scales of a %ux%u weight span more than 2^64 within a row group: "
+                             "beyond the GEMM's accumulator range (q35mm_matmul runs it on the GEMV)", w.rows, w.cols);
         if (!gemm_fits(w, m))
             return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
         ntiles += (w.nb + 1) / 2;

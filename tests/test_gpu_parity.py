@@ -442,3 +442,54 @@ def test_host_abi_from_several_threads(q, wl, gpu):
     assert not errors, errors
     for W, _ in Ws:
         q.release(W)
+
+
+def _scale_pattern(nb, kb, e_hi, e_lo):
+    """bf16 scales alternating 2^e_hi and 2^e_lo along K in every row group."""
+    sc = np.empty((nb, kb), np.uint16)
+    for j in range(kb):
+        e = e_hi if j % 2 == 0 else e_lo
+        sc[:, j] = (127 + e) << 7
+    return sc
+
+
+def test_gemm_wide_scale_spread_runs_on_gemv(q, oracle, wl, gpu):
+    """Block scales 2^60 and 2^-60 in one row group (bf16-representable):
+    the reference's lut*s*x stays finite, while a GEMM accumulator kept in
+    the current block's units would overflow.  q35_mm_fp8_batch at 96 tokens
+    (the GEMM range) runs such a weight on the GEMV and meets the GEMV bar;
+    q35mm_gemm refuses it."""
+    import torch
+    rng = np.random.default_rng(341)
+    W = rng.integers(0, 0x7E, size=(256, 1024), dtype=np.uint8) | (rng.integers(0, 2, size=(256, 1024), dtype=np.uint8) << 7)
+    sc = _scale_pattern(2, 8, 60, -60)
+    X = wl.gen_act(342, 96, 1024)
+    Y = q.mm_fp8_batch(W, sc, X)
+    Yr = oracle.mm_batch(W, sc, X)
+    assert np.isfinite(Yr).all() and np.isfinite(Y).all()
+    for t in range(96):
+        assert normwise_rel(Y[t], Yr[t]) <= GEMV_TOL, t
+    w = q.Weight(W, sc)
+    with pytest.raises(q.Q35mmError):
+        q.gemm(w, torch.from_numpy(X).to(gpu), torch.empty((96, 256), device=gpu))
+    w.free()
+    q.release(W)
+
+
+def test_gemm_scale_spread_2_pow_40(q, oracle, wl, gpu):
+    """Scales 2^20 and 2^-20 alternating along K (a spread of 2^40, inside
+    the GEMM's range): the GEMM with bf16-representable activations agrees
+    with the oracle far inside its bar."""
+    import torch
+    rng = np.random.default_rng(343)
+    W = rng.integers(0, 0x7E, size=(256, 1024), dtype=np.uint8) | (rng.integers(0, 2, size=(256, 1024), dtype=np.uint8) << 7)
+    sc = _scale_pattern(2, 8, 20, -20)
+    X = wl.gen_act(344, 96, 1024, bf16=True)
+    w = q.Weight(W, sc)
+    dY = torch.empty((96, 256), device=gpu)
+    q.gemm(w, torch.from_numpy(X).to(gpu), dY)
+    torch.cuda.synchronize()
+    Y = dY.cpu().numpy().astype(np.float64)
+    Yr = oracle.mm_batch(W, sc, X).astype(np.float64)
+    assert np.linalg.norm(Y - Yr) / np.linalg.norm(Yr) <= 1e-5
+    w.free()
