@@ -1,0 +1,205 @@
+// q35mm_probe.hip -- ceilings the kernels are measured against (not part of
+// libq35mm.so; built by build.py as lib/q35mm_probe).
+//
+//   q35mm_probe read [pool_MB]
+//     Raw read time of e4m3 weights of the decode projection shapes in the
+//     lane-order tiled layout (16 KiB per 128x128 block), no arithmetic:
+//       tiles  -- the row-split GEMV's decomposition: one workgroup per 32-row
+//                 sub-tile, four wavefronts splitting K, each loading one
+//                 1 KiB chunk per lane-order load through a ring of 2 or 3
+//                 K blocks (non-temporal loads, as the GEMV);
+//       linear -- the same bytes as one contiguous stream, 256 workgroups,
+//                 1 KiB per wavefront load, 8 loads in flight.
+//     Each launch reads a different copy of the weight from a pool of
+//     pool_MB (default 1536) so no cache holds it.  Prints us and GB/s.
+//
+//   q35mm_probe mfma
+//     Issue rate of v_mfma_f32_32x32x16_bf16: 256 workgroups of four
+//     wavefronts (one per SIMD), each wavefront issuing 8 independent
+//     accumulator chains of back-to-back MFMAs; also the core clock under
+//     that load (s_memtime ticks against s_memrealtime's 100 MHz).  Prints
+//     TFLOP/s and cycles per MFMA.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#define CK(x)                                                                                  \
+    do {                                                                                       \
+        hipError_t e_ = (x);                                                                   \
+        if (e_ != hipSuccess) {                                                                \
+            fprintf(stderr, "%s failed: %s (line %d)\n", #x, hipGetErrorString(e_), __LINE__); \
+            exit(1);                                                                           \
+        }                                                                                      \
+    } while (0)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ---- read: row-split decomposition ---------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void read_tiles(const uint8_t *codes, uint32_t kb, float *out) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t sub = blockIdx.x, g = sub >> 2, s = sub & 3;
+    const uint32_t k0 = wv * kb / 4, n = (wv + 1) * kb / 4 - k0;
+    const uint8_t *b = codes + ((size_t)g * kb * 4 + s) * 4096 + (size_t)k0 * 16384 + lane * 16;
+    u32x4 buf[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int d = 0; d < D; d++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min((uint32_t)d, n - 1) * 16384 + j * 1024));
+    for (uint32_t i = 0; i < n; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (i + d < n) acc += buf[d][j].x ^ buf[d][j].w;
+                buf[d][j] = __builtin_nontemporal_load(
+                    (const u32x4 *)(b + (size_t)min(i + d + D, n - 1) * 16384 + j * 1024));
+            }
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+}
+
+// ---- read: one contiguous stream -------------------------------------------
+__global__ __launch_bounds__(256) void read_linear(const uint8_t *codes, size_t bytes, float *out) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint64_t L = bytes / 1024;
+    const uint64_t l0 = (uint64_t)blockIdx.x * L / gridDim.x, l1 = (uint64_t)(blockIdx.x + 1) * L / gridDim.x;
+    const uint64_t w0 = l0 + wv * (l1 - l0) / 4, w1 = l0 + (wv + 1) * (l1 - l0) / 4;
+    uint32_t acc = 0;
+    if (w1 > w0) {
+        const uint32_t n = (uint32_t)(w1 - w0);
+        const uint8_t *b = codes + w0 * 1024 + lane * 16;
+        constexpr int D = 8;
+        u32x4 buf[D];
+#pragma unroll
+        for (int d = 0; d < D; d++) buf[d] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min((uint32_t)d, n - 1) * 1024));
+        for (uint32_t i = 0; i < n; i += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                if (i + d < n) acc += buf[d].x ^ buf[d].w;
+                buf[d] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min(i + d + D, n - 1) * 1024));
+            }
+        }
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+}
+
+// ---- MFMA issue rate ------------------------------------------------------
+__global__ __launch_bounds__(256) void mfma_rate(uint32_t iters, float *out, uint64_t *clocks) {
+    const uint32_t lane = threadIdx.x & 63;
+    bf16x8 a, b;
+    for (int i = 0; i < 8; i++) {
+        a[i] = (__bf16)(float)((lane + i) & 7);
+        b[i] = (__bf16)(float)((lane * 3 + i) & 7);
+    }
+    f32x16 acc[8] = {};
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+    for (int c = 0; c < 8; c++) s += acc[c][lane & 15];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clocks[blockIdx.x * 2] = t1 - t0;
+        clocks[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
+static float time_ms(hipEvent_t a, hipEvent_t b) {
+    float ms = 0.0f;
+    CK(hipEventElapsedTime(&ms, a, b));
+    return ms;
+}
+
+static int run_read(size_t pool_mb) {
+    struct Shape { const char *name; uint32_t k, n; };
+    const Shape shapes[] = {{"qkv 5120->6144", 5120, 6144},     {"o_proj 4096->5120", 4096, 5120},
+                            {"gate+up 5120->34816", 5120, 34816}, {"down 17408->5120", 17408, 5120},
+                            {"single 5120->5120", 5120, 5120}};
+    float *out;
+    CK(hipMalloc(&out, 1 << 20));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    for (const Shape &sh : shapes) {
+        const uint32_t nb = (sh.n + 127) / 128, kb = (sh.k + 127) / 128;
+        const size_t bytes = (size_t)nb * kb * 16384;
+        const int copies = std::max<int>(4, (int)(pool_mb * 1000000 / bytes));
+        uint8_t *pool;
+        CK(hipMalloc(&pool, bytes * copies));
+        CK(hipMemset(pool, 0x35, bytes * copies));
+        const uint32_t subs = (sh.n + 31) / 32;
+        for (int variant = 0; variant < 3; variant++) {
+            auto launch = [&](int i) {
+                const uint8_t *c = pool + (size_t)(i % copies) * bytes;
+                if (variant == 0) hipLaunchKernelGGL(read_tiles<2>, dim3(subs), dim3(256), 0, 0, c, kb, out);
+                else if (variant == 1) hipLaunchKernelGGL(read_tiles<3>, dim3(subs), dim3(256), 0, 0, c, kb, out);
+                else hipLaunchKernelGGL(read_linear, dim3(256), dim3(256), 0, 0, c, bytes, out);
+            };
+            for (int i = 0; i < 8; i++) launch(i);
+            CK(hipDeviceSynchronize());
+            const int reps = 200;
+            CK(hipEventRecord(e0));
+            for (int i = 0; i < reps; i++) launch(i);
+            CK(hipEventRecord(e1));
+            CK(hipEventSynchronize(e1));
+            const double us = time_ms(e0, e1) * 1e3 / reps;
+            printf("read %-22s %-8s %8.2f us %7.0f GB/s (%zu bytes, %d copies)\n", sh.name,
+                   variant == 0 ? "tiles/2" : variant == 1 ? "tiles/3" : "linear", us, bytes / us / 1e3, bytes,
+                   copies);
+            fflush(stdout);
+        }
+        CK(hipFree(pool));
+    }
+    return 0;
+}
+
+static int run_mfma() {
+    const uint32_t blocks = 256, iters = 4096;
+    float *out;
+    uint64_t *clk;
+    CK(hipMalloc(&out, blocks * 256 * sizeof(float)));
+    CK(hipMalloc(&clk, blocks * 2 * sizeof(uint64_t)));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, 0, 64u, out, clk);
+    CK(hipDeviceSynchronize());
+    CK(hipEventRecord(e0));
+    hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, 0, iters, out, clk);
+    CK(hipEventRecord(e1));
+    CK(hipEventSynchronize(e1));
+    const double s = time_ms(e0, e1) * 1e-3;
+    std::vector<uint64_t> c(blocks * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    double cyc = 0, real = 0;
+    for (uint32_t b = 0; b < blocks; b++) {
+        cyc += (double)c[2 * b];
+        real += (double)c[2 * b + 1];
+    }
+    const double mfmas = (double)blocks * 4 * iters * 8;
+    const double flops = mfmas * 32 * 32 * 16 * 2;
+    const double clock_ghz = cyc / real * 0.1;   // s_memrealtime ticks at 100 MHz
+    printf("mfma 32x32x16 bf16: %.1f TFLOP/s over %.3f ms; core clock under load %.2f GHz; "
+           "%.1f cycles per MFMA per SIMD\n",
+           flops / s / 1e12, s * 1e3, clock_ghz, cyc / blocks / (iters * 8.0));
+    return 0;
+}
+
+int main(int argc, char **argv) {
+    if (argc >= 2 && !strcmp(argv[1], "read")) return run_read(argc >= 3 ? strtoul(argv[2], nullptr, 10) : 1536);
+    if (argc >= 2 && !strcmp(argv[1], "mfma")) return run_mfma();
+    fprintf(stderr, "usage: %s read [pool_MB] | mfma\n", argv[0]);
+    return 2;
+}
