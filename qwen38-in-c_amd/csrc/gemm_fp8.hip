@@ -200,25 +200,30 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         const uint32_t nbk = min(nt * 2 + n32 / 4, sg.nb - 1);
         boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
     }
-    auto issue = [&](uint32_t st, uint32_t buf) {
+    // Copy k of stage st into ring slot buf: k < kALoads an A piece, then the
+    // B pieces.
+    auto issue_piece = [&](uint32_t st, uint32_t buf, uint32_t k) {
         const uint32_t kb = st >> 1, h = st & 1;
         lds_u8 *la = ring + buf * kStageBytes;
-#pragma unroll
-        for (uint32_t i = 0; i < kALoads; i++)
-            dma_1k(xa + (aoff[i] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
-                   la + (wv * kALoads + i) * kChunkBytes);
-#pragma unroll
-        for (uint32_t i = 0; i < kBLoads; i++)
+        if (k < kALoads) {
+            dma_1k(xa + (aoff[k] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
+                   la + (wv * kALoads + k) * kChunkBytes);
+        } else {
+            const uint32_t i = k - kALoads;
             dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
                    la + kStageA + (wv * kBLoads + i) * kChunkBytes);
+        }
+    };
+    auto issue = [&](uint32_t st, uint32_t buf) {
+#pragma unroll
+        for (uint32_t k = 0; k < kStageLoads; k++) issue_piece(st, buf, k);
     };
 
     // ---- block scales of the tile's two row groups, staged in LDS ----
-    // Read from LDS inside the loop they keep the LDS counter in order (a
-    // scalar load completing out of order would force full waits) and stay
-    // off the vmcnt queue that counts the stage copies.  0 past the last row
-    // group.  Done before the first copy is issued, so this barrier drains
-    // nothing.
+    // The loop takes them from registers (one K block per lane, refilled
+    // every 64 blocks), so no LDS read of a scale sits between its MFMAs and
+    // nothing waits for one there.  0 past the last row group.  Done before
+    // the first copy is issued, so this barrier drains nothing.
     float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
     for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
         const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
@@ -229,118 +234,140 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     }
     __syncthreads();
     const float *my_sc = sc_lds + (wn >> 1) * kGemmMaxSliceKb - kb0;   // indexed by kb
+    uint32_t sc_base = kb0;                                           // lane i holds block sc_base + i
+    float sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
+    auto scale_of = [&](uint32_t kb) {   // kb in [sc_base, sc_base + 64)
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), kb - sc_base));
+    };
 
     f32x16_t acc[4][2] = {};
     float s_prev = 0.0f;
 
     // Operands of one 32-column chunk: A for this wavefront's 4 token
     // sub-tiles x 2 MFMA halves (bf16), B for its 2 weight sub-tiles (16 e4m3
-    // codes per lane, both halves).
+    // codes per lane, both halves).  Read from LDS one piece at a time:
+    // piece k < 8 is A (i = k / 2, q = k % 2), pieces 8 and 9 are B.
     struct Frags {
         bf16x8_t a[4][2];
         u32x4_t b[2];
     };
-    auto read_frags = [&](Frags &f, uint32_t buf, uint32_t jj) {
+    auto read_piece = [&](Frags &f, uint32_t buf, uint32_t jj, uint32_t k) {
         const uint8_t *la = lds + buf * kStageBytes;
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-            for (uint32_t q = 0; q < 2; q++)
-                f.a[i][q] = *reinterpret_cast<const bf16x8_t *>(
-                    la + (((wm * 4 + i) * 2 + jj) * 2 + q) * kChunkBytes + lane * 16);
-#pragma unroll
-        for (uint32_t jn = 0; jn < 2; jn++)
-            f.b[jn] = *reinterpret_cast<const u32x4_t *>(
-                la + kStageA + ((wn * 2 + jn) * 2 + jj) * kChunkBytes + lane * 16);
+        if (k < 8) {
+            const uint32_t i = k >> 1, q = k & 1;
+            f.a[i][q] = *reinterpret_cast<const bf16x8_t *>(la + (((wm * 4 + i) * 2 + jj) * 2 + q) * kChunkBytes +
+                                                            lane * 16);
+        } else {
+            const uint32_t jn = k - 8;
+            f.b[jn] = *reinterpret_cast<const u32x4_t *>(la + kStageA + ((wn * 2 + jn) * 2 + jj) * kChunkBytes +
+                                                         lane * 16);
+        }
     };
-    // 16 MFMAs; the two halves of a chunk are issued 8 apart so no MFMA waits
-    // for the one before it.  keep is the conversion's power-of-two scale:
-    // 1.0 (exact) for a live block, 0.0 (= 2^-127) for a block whose scale is
-    // 0, which then adds at most 2^-127 * 448 * |x| per term (and NaN for a
-    // NaN code, as lut[code] * 0 does).
-    auto mma = [&](const Frags &f, bool rescale, float r, float keep) {
+    constexpr uint32_t kPieces = 10;
+    static_assert(kStageLoads + kPieces == 16, "one copy or read per MFMA of a phase");
+    // Accumulator a = 2i + jn (MFMA tile i, jn) brought into new units.
+    auto rescale = [&](uint32_t a, float r) { acc[a >> 1][a & 1] *= r; };
+
+    // One phase: the 16 MFMAs of chunk operands f, in the order q, i, jn (the
+    // two halves of a chunk 8 MFMAs apart, so no MFMA waits for the one
+    // before it), each followed by slot(t): the phase's other work, pinned
+    // one piece per MFMA (sched_barrier) -- an LDS read or stage copy for the
+    // next phase, a rescale.  Issued back to back before the MFMAs instead,
+    // those reads and copies stall a wavefront that meets a full LDS queue
+    // with its MFMAs still unissued (the same kernel with them, and only
+    // them, removed ran 44 us faster on 512 x 34816 x 5120).  keep is the
+    // conversion's power-of-two scale: 1.0 (exact) for a live block, 0.0 (=
+    // 2^-127) for a block whose scale is 0, which then adds at most 2^-127 *
+    // 448 * |x| per term (and NaN for a NaN code, as lut[code] * 0 does).
+    auto phase = [&](const Frags &f, float keep, auto &&slot) {
         bf16x8_t bw[2][2];
 #pragma unroll
-        for (uint32_t jn = 0; jn < 2; jn++) {
-            bw[jn][0] = e4m3x8_to_bf16x8_cvt(f.b[jn][0], f.b[jn][1], keep);
-            bw[jn][1] = e4m3x8_to_bf16x8_cvt(f.b[jn][2], f.b[jn][3], keep);
+        for (uint32_t jn = 0; jn < 2; jn++) bw[jn][0] = e4m3x8_to_bf16x8_cvt(f.b[jn][0], f.b[jn][1], keep);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t t = 0; t < 16; t++) {
+            const uint32_t q = t >> 3, i = (t >> 1) & 3, jn = t & 1;
+            acc[i][jn] = mfma32x32x16(f.a[i][q], bw[jn][q], acc[i][jn]);
+            if (t == 1) {
+#pragma unroll
+                for (uint32_t j = 0; j < 2; j++) bw[j][1] = e4m3x8_to_bf16x8_cvt(f.b[j][2], f.b[j][3], keep);
+            }
+            slot(t);
+            __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (uint32_t q = 0; q < 2; q++)
-#pragma unroll
-            for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-                for (uint32_t jn = 0; jn < 2; jn++) {
-                    if (q == 0 && rescale) acc[i][jn] *= r;
-                    acc[i][jn] = mfma32x32x16(f.a[i][q], bw[jn][q], acc[i][jn]);
-                }
     };
 
     // ---- pipeline ----
-    // LDS ring of three stages.  Stage s: its first chunk's operands are in
-    // registers (f0) when it starts; the second chunk's are read (f1) while
-    // the first chunk's MFMAs run.  Then, once every wavefront has read all of
-    // stage s and stage s+1 has landed (one barrier), stage s+3 is copied
-    // into s's slot and stage s+1's first chunk is read while the second
-    // chunk's MFMAs run.  Every wavefront issues exactly kStageLoads copies
-    // per stage (clamped to the last stage past the end), so
-    // "vmcnt <= kStageLoads" means: all but the newest stage have landed.
+    // LDS ring of three stages (64 columns each, two per K block).  Stage s:
+    // its first chunk's operands are in registers (f0) when it starts; the
+    // second chunk's are read (f1) during the first chunk's MFMAs.  Then,
+    // once every wavefront has read all of stage s and stage s+1 has landed
+    // (one barrier), stage s+3 is copied into s's slot and stage s+1's first
+    // chunk is read during the second chunk's MFMAs.  Every wavefront issues
+    // exactly kStageLoads copies per stage (clamped to the last stage past
+    // the end), so "vmcnt <= kStageLoads" means: all but the newest stage
+    // have landed.
+    //
+    // Block scales: the accumulator is kept in units of the last live block
+    // scale.  Before the MFMAs of block kb+1 it is multiplied by r = s_prev /
+    // s_{kb+1}: accumulators 0..5 in the last phase of block kb, two MFMAs
+    // after their last MFMA of the block; 6 and 7 in the first phase of block
+    // kb+1, before their first.  Each accumulator sees the same products in
+    // the same order as with one multiply at the block boundary.  A block
+    // with scale 0 runs with keep = 0 and r = 1, so the accumulator keeps its
+    // units.  No branches around the MFMAs.
     issue(st0, 0);
     issue(min(st0 + 1, st1 - 1), 1);
     issue(min(st0 + 2, st1 - 1), 2);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
     lds_barrier();
     Frags f0, f1;
-    read_frags(f0, 0, 0);
+#pragma unroll
+    for (uint32_t k = 0; k < kPieces; k++) read_piece(f0, 0, 0, k);
     uint32_t buf = 0;
-    // No branches around the MFMAs: a block with scale 0 runs with keep = 0
-    // and r = 1, so the accumulator keeps its units.
-    // sched_barrier(0) pins the phases: the compiler would otherwise sink each
-    // LDS read next to its MFMA and wait for it there.  The next K block's
-    // scale is read with the f1 operands and its rescale factor computed after
-    // the MFMAs were issued, so neither waits.
-    float sc0 = my_sc[kb0];
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    bool live = sc0 != 0.0f;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f0 and the first scales
+    const float sc0 = scale_of(kb0);
+    const bool live = sc0 != 0.0f;
     float keep = live ? 1.0f : 0.0f;
     float r = live ? 0.0f : 1.0f;            // the accumulator is still zero
     s_prev = live ? sc0 : 0.0f;              // units of the accumulator after this block
     for (uint32_t kb = kb0; kb < kb1; kb++) {
-        bool live_n = false;
-        float keep_n = 0.0f;
-        float r_n = 1.0f, s_prev_n = s_prev;
+        // the next block's scale and rescale factor (registers only, except
+        // one LDS refill every 64 blocks)
+        if (kb + 1 == sc_base + 64) {
+            sc_base += 64;
+            sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        }
+        const bool live_n = kb + 1 < kb1 && scale_of(min(kb + 1, kb1 - 1)) != 0.0f;
+        const float sc_n = live_n ? scale_of(kb + 1) : 1.0f;
+        const float keep_n = live_n ? 1.0f : 0.0f;
+        const float r_n = live_n ? (s_prev != 0.0f ? s_prev / sc_n : 0.0f) : 1.0f;
+        const float s_prev_n = live_n ? sc_n : s_prev;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (uint32_t h = 0; h < 2; h++) {
             const uint32_t s = 2 * kb + h;
-            // f0 was read a whole MFMA phase ago.  Waiting for it here, before
-            // f1's reads are issued, keeps the MFMAs below free of waits (the
-            // compiler cannot count LDS reads past the LDS copies and would
-            // otherwise wait for f1 too).
+            // f0 was read during the previous phase
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-            read_frags(f1, buf, 1);
-            float sc_n = 0.0f;
-            if (h == 0) sc_n = my_sc[min(kb + 1, kb1 - 1)];
-            __builtin_amdgcn_sched_barrier(0);
-            mma(f0, h == 0, r, keep);
-            __builtin_amdgcn_sched_barrier(0);
-            if (h == 0) {
-                live_n = kb + 1 < kb1 && sc_n != 0.0f;
-                keep_n = live_n ? 1.0f : 0.0f;
-                r_n = live_n ? (s_prev != 0.0f ? s_prev / sc_n : 0.0f) : 1.0f;
-                s_prev_n = live_n ? sc_n : s_prev;
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            phase(f0, keep, [&](uint32_t t) {
+                if (t < kPieces) read_piece(f1, buf, 1, t);
+                if (h == 0 && t < 2) rescale(6 + t, r);
+            });
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f1 is in registers: slot s is free
             lds_barrier();
-            issue(min(s + 3, st1 - 1), buf);
-            buf = buf == 2 ? 0 : buf + 1;
-            read_frags(f0, buf, 0);                    // past the end: unused, in bounds
-            __builtin_amdgcn_sched_barrier(0);
-            mma(f1, false, 1.0f, keep);
-            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t nb = buf == 2 ? 0 : buf + 1;
+            const uint32_t st_copy = min(s + 3, st1 - 1);
+            phase(f1, keep, [&](uint32_t t) {
+                if (t < kStageLoads)
+                    issue_piece(st_copy, buf, t);
+                else
+                    read_piece(f0, nb, 0, t - kStageLoads);   // past the end: unused, in bounds
+                if (h == 1 && t >= 10) rescale(t - 10, r_n);
+            });
+            buf = nb;
         }
-        live = live_n;
         keep = keep_n;
         r = r_n;
         s_prev = s_prev_n;

@@ -13,6 +13,12 @@
 //     Each launch reads a different copy of the weight from a pool of
 //     pool_MB (default 1536) so no cache holds it.  Prints us and GB/s.
 //
+//   q35mm_probe lds
+//     LDS read rate of ds_read_b128 (conflict-free: lane l reads 16 bytes at
+//     l*16 of a 1 KiB row) from 256 workgroups of 8 wavefronts, each
+//     wavefront issuing 8 independent reads per iteration; prints bytes per
+//     clock per CU (core clock from s_memtime against s_memrealtime).
+//
 //   q35mm_probe mfma
 //     Issue rate of v_mfma_f32_32x32x16_bf16: 256 workgroups of four
 //     wavefronts (one per SIMD), each wavefront issuing 8 independent
@@ -116,6 +122,31 @@ __global__ __launch_bounds__(256) void mfma_rate(uint32_t iters, float *out, uin
     }
 }
 
+// ---- LDS read rate -------------------------------------------------------
+__global__ __launch_bounds__(512) void lds_rate(uint32_t iters, float *out, uint64_t *clocks) {
+    __shared__ __align__(16) uint8_t buf[64 * 1024];
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < 64 * 1024 / 16; i += 512)
+        reinterpret_cast<u32x4 *>(buf)[i] = u32x4{i, i * 3u, i * 5u, i * 7u};
+    __syncthreads();
+    u32x4 acc = {0, 0, 0, 0};
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; it++) {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)   // rows (it*8 + j + wv) % 64 of 1 KiB: always inside buf
+            v[j] = *reinterpret_cast<const u32x4 *>(buf + ((it * 8 + j + wv) & 63) * 1024 + lane * 16);
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc ^= v[j];
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    out[blockIdx.x * 512 + threadIdx.x] = (float)(acc.x ^ acc.y ^ acc.z ^ acc.w);
+    if (threadIdx.x == 0) {
+        clocks[blockIdx.x * 2] = t1 - t0;
+        clocks[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
 static float time_ms(hipEvent_t a, hipEvent_t b) {
     float ms = 0.0f;
     CK(hipEventElapsedTime(&ms, a, b));
@@ -197,9 +228,35 @@ static int run_mfma() {
     return 0;
 }
 
+static int run_lds() {
+    const uint32_t blocks = 256, iters = 4096;
+    float *out;
+    uint64_t *clk;
+    CK(hipMalloc(&out, blocks * 512 * sizeof(float)));
+    CK(hipMalloc(&clk, blocks * 2 * sizeof(uint64_t)));
+    hipLaunchKernelGGL(lds_rate, dim3(blocks), dim3(512), 0, 0, 64u, out, clk);
+    CK(hipDeviceSynchronize());
+    hipLaunchKernelGGL(lds_rate, dim3(blocks), dim3(512), 0, 0, iters, out, clk);
+    CK(hipDeviceSynchronize());
+    std::vector<uint64_t> c(blocks * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    double cyc = 0, real = 0;
+    for (uint32_t b = 0; b < blocks; b++) {
+        cyc += (double)c[2 * b];
+        real += (double)c[2 * b + 1];
+    }
+    cyc /= blocks;
+    real /= blocks;
+    const double bytes_per_cu = 8.0 * iters * 8 * 1024;   // 8 wavefronts x iters x 8 reads x 1 KiB
+    printf("lds ds_read_b128: %.1f bytes per clock per CU (%.0f cycles per workgroup, core clock %.2f GHz)\n",
+           bytes_per_cu / cyc, cyc, cyc / real * 0.1);
+    return 0;
+}
+
 int main(int argc, char **argv) {
     if (argc >= 2 && !strcmp(argv[1], "read")) return run_read(argc >= 3 ? strtoul(argv[2], nullptr, 10) : 1536);
     if (argc >= 2 && !strcmp(argv[1], "mfma")) return run_mfma();
-    fprintf(stderr, "usage: %s read [pool_MB] | mfma\n", argv[0]);
+    if (argc >= 2 && !strcmp(argv[1], "lds")) return run_lds();
+    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma\n", argv[0]);
     return 2;
 }
