@@ -10,7 +10,9 @@
 //    tiles, 1 KiB per MFMA operand load).
 //  - A workgroup computes a 256x256 output tile with eight wavefronts of
 //    128 (tokens) x 64 (weight rows), two per SIMD: 8 accumulators of 32x32,
-//    128 VGPRs, so the per-block rescale below is a plain v_mul.
+//    128 VGPRs, so the per-block rescale below is a plain v_mul.  (64 x 128
+//    wavefront tiles read 20% fewer LDS bytes per MFMA but convert twice the
+//    e4m3 codes; they ran 4% slower.)
 //  - K advances in stages of 64 columns (two 32-column chunks).  A stage is
 //    48 KiB of LDS: A as bf16 (32 KiB) and B still as e4m3 (16 KiB); B is
 //    widened to bf16 after the LDS read, exactly.  Stages are copied straight
@@ -21,12 +23,18 @@
 //    accumulator is kept in units of the last nonzero scale: before block kb
 //    it is multiplied by s_prev / s_kb, after the last block by s_last.  One
 //    v_mul per accumulator and K block, and the scale is never folded into
-//    bf16 weights (that would round).  A block with scale 0 contributes
-//    nothing and is skipped.
-//  - Work split: whole rounds of tiles unsplit, the tiles of a last partial
-//    round cut along K; their partial tiles are added in slice order by a
-//    second kernel (deterministic, spread over the whole device).
+//    bf16 weights (that would round).  The multiplies and the conversions are
+//    spread over the MFMAs (at most five and one per MFMA), never in bursts.
+//  - Work split: whole rounds of tiles unsplit; the tiles of a last partial
+//    round either cut into 64x64 tiles, run by the whole-tile workgroups
+//    after their own tile while its stores drain (or by gemm_tail_kernel
+//    when there is no whole round), or cut along K, their partial tiles added
+//    in slice order by a second kernel (deterministic, spread over the whole
+//    device).
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+#include <utility>
 
 #include "q35mm_device.h"
 #include "q35mm_internal.h"
@@ -86,6 +94,69 @@ __device__ __forceinline__ TileAt tile_at(const GemmParams &p, uint32_t tile) {
     const uint32_t lt = MULTI ? tile - p.seg[s].tile0 : tile;
     return {s, lt % p.mtiles, lt / p.mtiles};
 }
+
+// s_waitcnt immediate that waits only for lgkmcnt <= n.
+constexpr uint32_t waitcnt_lgkm(uint32_t n) { return 15u | (3u << 14) | (7u << 4) | ((n & 15u) << 8); }
+
+// One v_cvt_scalef32_pk_bf16_fp8: codes 0,1 (HI false) or 2,3 (HI true) of w
+// to two bf16, packed.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_pk(uint32_t w, float keep) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, keep, HI));
+}
+
+// f(std::integral_constant<uint32_t, I>) for I = 0..N-1, each call its own
+// code (indices known at compile time, whatever the unroller decides).
+template <class F, uint32_t... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<uint32_t, I...>) {
+    (f(std::integral_constant<uint32_t, I>{}), ...);
+}
+template <uint32_t N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<uint32_t, N>{});
+}
+
+// Where the per-K-block rescale goes.  Accumulator a runs MFMAs
+// 2a and 2a+1 of every 16-MFMA phase, so between its last MFMA of block kb
+// (slot 2a+1 of the block's last phase) and its first of block kb+1 (slot 2a
+// of the next phase) lie 14 slots; its 16 values are multiplied in slots
+// 2a+3 .. 2a+15 of the 32 (last phase: g = t, next phase: g = 16 + t), at
+// most five multiplies per slot, earliest window first.  Issued in one burst
+// after one MFMA, 16 multiplies hold back the wavefront's next MFMA by ~64
+// cycles; five fit beside the 32-cycle MFMA.
+struct RescalePlan {
+    uint8_t cnt[32][8];
+    uint8_t first[32][8];
+};
+constexpr uint32_t kRescaleCap = 5;
+constexpr RescalePlan make_rescale_plan() {
+    RescalePlan pl{};
+    uint32_t done[8] = {};
+    for (uint32_t g = 0; g < 32; g++) {
+        uint32_t cap = kRescaleCap;
+        for (uint32_t a = 0; a < 8; a++) {
+            pl.cnt[g][a] = 0;
+            pl.first[g][a] = 0;
+            if (g < 2 * a + 3 || g > 2 * a + 15 || cap == 0) continue;
+            const uint32_t n = cap < 16 - done[a] ? cap : 16 - done[a];
+            pl.cnt[g][a] = (uint8_t)n;
+            pl.first[g][a] = (uint8_t)done[a];
+            done[a] += n;
+            cap -= n;
+        }
+    }
+    return pl;
+}
+constexpr RescalePlan kRescale = make_rescale_plan();
+constexpr bool rescale_plan_complete() {
+    uint32_t tot[8] = {};
+    for (uint32_t g = 0; g < 32; g++)
+        for (uint32_t a = 0; a < 8; a++) tot[a] += kRescale.cnt[g][a];
+    for (uint32_t a = 0; a < 8; a++)
+        if (tot[a] != 16) return false;
+    return true;
+}
+static_assert(rescale_plan_complete(), "every accumulator value rescaled once per K block");
 
 }  // namespace
 
@@ -155,267 +226,6 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
     }
 }
 
-template <bool MULTI>
-__global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    lds_u8 *const ring = (lds_u8 *)lds;
-
-    const bool split = blockIdx.x >= p.split_tile0;
-    const uint32_t S = split ? p.nslices : 1;
-    const uint32_t u = split ? blockIdx.x - p.split_tile0 : 0;
-    const uint32_t tile = split ? p.split_tile0 + u / S : blockIdx.x;
-    const uint32_t sl = split ? u % S : 0;
-    const TileAt ta = tile_at<MULTI>(p, tile);
-    const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t mt = ta.mt, nt = ta.nt;
-    const uint32_t KB = p.kb;
-    const uint32_t kb0 = (sl * KB) / S, kb1 = ((sl + 1) * KB) / S;
-    const uint32_t st0 = 2 * kb0, st1 = 2 * kb1;   // stages of 64 columns
-
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wm = wv & 1, wn = wv >> 1;   // 2 x 4 wavefronts of 128 x 64
-
-    // ---- global sources of this wavefront's pieces ----
-    // A piece P (0..31): token rows (mt*8 + P/4)*32.., piece (h*4 + P%4) of the
-    // K block's eight (h = stage half); wavefront w copies 4w..4w+3.
-    // B piece Q (0..15): weight rows (nt*8 + Q/2)*32.., chunk 2h + Q%2;
-    // wavefront w copies 2w, 2w+1.  A missing second row group (odd NB)
-    // reads the last group instead; those columns are never stored.
-    const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb);
-    // Byte offsets (32-bit: the host keeps both operands under 4 GiB) that are
-    // wavefront-uniform, so they live in scalar registers; each copy adds the
-    // lane's 16 bytes and uses the global_load_lds saddr + voffset form.
-    uint32_t aoff[kALoads], boff[kBLoads];
-    const uint32_t lane16 = lane * 16;
-#pragma unroll
-    for (uint32_t i = 0; i < kALoads; i++) {
-        const uint32_t P = wv * kALoads + i;
-        aoff[i] = (mt * 8 + P / 4) * (KB * 8 * kChunkBytes) + (P % 4) * kChunkBytes;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kBLoads; i++) {
-        const uint32_t Q = wv * kBLoads + i;
-        const uint32_t n32 = Q / 2;
-        const uint32_t nbk = min(nt * 2 + n32 / 4, sg.nb - 1);
-        boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
-    }
-    // Copy k of stage st into ring slot buf: k < kALoads an A piece, then the
-    // B pieces.
-    auto issue_piece = [&](uint32_t st, uint32_t buf, uint32_t k) {
-        const uint32_t kb = st >> 1, h = st & 1;
-        lds_u8 *la = ring + buf * kStageBytes;
-        if (k < kALoads) {
-            dma_1k(xa + (aoff[k] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
-                   la + (wv * kALoads + k) * kChunkBytes);
-        } else {
-            const uint32_t i = k - kALoads;
-            dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
-                   la + kStageA + (wv * kBLoads + i) * kChunkBytes);
-        }
-    };
-    auto issue = [&](uint32_t st, uint32_t buf) {
-#pragma unroll
-        for (uint32_t k = 0; k < kStageLoads; k++) issue_piece(st, buf, k);
-    };
-
-    // ---- block scales of the tile's two row groups, staged in LDS ----
-    // The loop takes them from registers (one K block per lane, refilled
-    // every 64 blocks), so no LDS read of a scale sits between its MFMAs and
-    // nothing waits for one there.  0 past the last row group.  Done before
-    // the first copy is issued, so this barrier drains nothing.
-    float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
-    for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
-        const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
-        const uint32_t nbg = nt * 2 + g;
-        float v = 0.0f;
-        if (nbg < sg.nb && kk < kb1 - kb0) v = sg.scale[(size_t)nbg * KB + kb0 + kk];
-        sc_lds[j] = v;
-    }
-    __syncthreads();
-    const float *my_sc = sc_lds + (wn >> 1) * kGemmMaxSliceKb - kb0;   // indexed by kb
-    uint32_t sc_base = kb0;                                           // lane i holds block sc_base + i
-    float sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
-    auto scale_of = [&](uint32_t kb) {   // kb in [sc_base, sc_base + 64)
-        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), kb - sc_base));
-    };
-
-    f32x16_t acc[4][2] = {};
-    float s_prev = 0.0f;
-
-    // Operands of one 32-column chunk: A for this wavefront's 4 token
-    // sub-tiles x 2 MFMA halves (bf16), B for its 2 weight sub-tiles (16 e4m3
-    // codes per lane, both halves).  Read from LDS one piece at a time:
-    // piece k < 8 is A (i = k / 2, q = k % 2), pieces 8 and 9 are B.
-    struct Frags {
-        bf16x8_t a[4][2];
-        u32x4_t b[2];
-    };
-    auto read_piece = [&](Frags &f, uint32_t buf, uint32_t jj, uint32_t k) {
-        const uint8_t *la = lds + buf * kStageBytes;
-        if (k < 8) {
-            const uint32_t i = k >> 1, q = k & 1;
-            f.a[i][q] = *reinterpret_cast<const bf16x8_t *>(la + (((wm * 4 + i) * 2 + jj) * 2 + q) * kChunkBytes +
-                                                            lane * 16);
-        } else {
-            const uint32_t jn = k - 8;
-            f.b[jn] = *reinterpret_cast<const u32x4_t *>(la + kStageA + ((wn * 2 + jn) * 2 + jj) * kChunkBytes +
-                                                         lane * 16);
-        }
-    };
-    constexpr uint32_t kPieces = 10;
-    static_assert(kStageLoads + kPieces == 16, "one copy or read per MFMA of a phase");
-    // Accumulator a = 2i + jn (MFMA tile i, jn) brought into new units.
-    auto rescale = [&](uint32_t a, float r) { acc[a >> 1][a & 1] *= r; };
-
-    // One phase: the 16 MFMAs of chunk operands f, in the order q, i, jn (the
-    // two halves of a chunk 8 MFMAs apart, so no MFMA waits for the one
-    // before it), each followed by slot(t): the phase's other work, pinned
-    // one piece per MFMA (sched_barrier) -- an LDS read or stage copy for the
-    // next phase, a rescale.  Issued back to back before the MFMAs instead,
-    // those reads and copies stall a wavefront that meets a full LDS queue
-    // with its MFMAs still unissued (the same kernel with them, and only
-    // them, removed ran 44 us faster on 512 x 34816 x 5120).  keep is the
-    // conversion's power-of-two scale: 1.0 (exact) for a live block, 0.0 (=
-    // 2^-127) for a block whose scale is 0, which then adds at most 2^-127 *
-    // 448 * |x| per term (and NaN for a NaN code, as lut[code] * 0 does).
-    auto phase = [&](const Frags &f, float keep, auto &&slot) {
-        bf16x8_t bw[2][2];
-#pragma unroll
-        for (uint32_t jn = 0; jn < 2; jn++) bw[jn][0] = e4m3x8_to_bf16x8_cvt(f.b[jn][0], f.b[jn][1], keep);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (uint32_t t = 0; t < 16; t++) {
-            const uint32_t q = t >> 3, i = (t >> 1) & 3, jn = t & 1;
-            acc[i][jn] = mfma32x32x16(f.a[i][q], bw[jn][q], acc[i][jn]);
-            if (t == 1) {
-#pragma unroll
-                for (uint32_t j = 0; j < 2; j++) bw[j][1] = e4m3x8_to_bf16x8_cvt(f.b[j][2], f.b[j][3], keep);
-            }
-            slot(t);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    // ---- pipeline ----
-    // LDS ring of three stages (64 columns each, two per K block).  Stage s:
-    // its first chunk's operands are in registers (f0) when it starts; the
-    // second chunk's are read (f1) during the first chunk's MFMAs.  Then,
-    // once every wavefront has read all of stage s and stage s+1 has landed
-    // (one barrier), stage s+3 is copied into s's slot and stage s+1's first
-    // chunk is read during the second chunk's MFMAs.  Every wavefront issues
-    // exactly kStageLoads copies per stage (clamped to the last stage past
-    // the end), so "vmcnt <= kStageLoads" means: all but the newest stage
-    // have landed.
-    //
-    // Block scales: the accumulator is kept in units of the last live block
-    // scale.  Before the MFMAs of block kb+1 it is multiplied by r = s_prev /
-    // s_{kb+1}: accumulators 0..5 in the last phase of block kb, two MFMAs
-    // after their last MFMA of the block; 6 and 7 in the first phase of block
-    // kb+1, before their first.  Each accumulator sees the same products in
-    // the same order as with one multiply at the block boundary.  A block
-    // with scale 0 runs with keep = 0 and r = 1, so the accumulator keeps its
-    // units.  No branches around the MFMAs.
-    issue(st0, 0);
-    issue(min(st0 + 1, st1 - 1), 1);
-    issue(min(st0 + 2, st1 - 1), 2);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
-    lds_barrier();
-    Frags f0, f1;
-#pragma unroll
-    for (uint32_t k = 0; k < kPieces; k++) read_piece(f0, 0, 0, k);
-    uint32_t buf = 0;
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f0 and the first scales
-    const float sc0 = scale_of(kb0);
-    const bool live = sc0 != 0.0f;
-    float keep = live ? 1.0f : 0.0f;
-    float r = live ? 0.0f : 1.0f;            // the accumulator is still zero
-    s_prev = live ? sc0 : 0.0f;              // units of the accumulator after this block
-    for (uint32_t kb = kb0; kb < kb1; kb++) {
-        // the next block's scale and rescale factor (registers only, except
-        // one LDS refill every 64 blocks)
-        if (kb + 1 == sc_base + 64) {
-            sc_base += 64;
-            sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-        }
-        const bool live_n = kb + 1 < kb1 && scale_of(min(kb + 1, kb1 - 1)) != 0.0f;
-        const float sc_n = live_n ? scale_of(kb + 1) : 1.0f;
-        const float keep_n = live_n ? 1.0f : 0.0f;
-        const float r_n = live_n ? (s_prev != 0.0f ? s_prev / sc_n : 0.0f) : 1.0f;
-        const float s_prev_n = live_n ? sc_n : s_prev;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (uint32_t h = 0; h < 2; h++) {
-            const uint32_t s = 2 * kb + h;
-            // f0 was read during the previous phase
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-            phase(f0, keep, [&](uint32_t t) {
-                if (t < kPieces) read_piece(f1, buf, 1, t);
-                if (h == 0 && t < 2) rescale(6 + t, r);
-            });
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f1 is in registers: slot s is free
-            lds_barrier();
-            const uint32_t nb = buf == 2 ? 0 : buf + 1;
-            const uint32_t st_copy = min(s + 3, st1 - 1);
-            phase(f1, keep, [&](uint32_t t) {
-                if (t < kStageLoads)
-                    issue_piece(st_copy, buf, t);
-                else
-                    read_piece(f0, nb, 0, t - kStageLoads);   // past the end: unused, in bounds
-                if (h == 1 && t >= 10) rescale(t - 10, r_n);
-            });
-            buf = nb;
-        }
-        keep = keep_n;
-        r = r_n;
-        s_prev = s_prev_n;
-    }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));   // no copy outlives the loop
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-        for (uint32_t jn = 0; jn < 2; jn++) acc[i][jn] *= s_prev;
-
-    // Output coordinates of accumulator element (i, jn, r) of this lane.
-    auto out_row = [&](uint32_t i, uint32_t r) -> uint32_t {
-        return wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    };
-    auto out_col = [&](uint32_t jn) -> uint32_t { return wn * 64 + jn * 32 + (lane & 31); };
-
-    if (!split) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-            for (uint32_t jn = 0; jn < 2; jn++)
-#pragma unroll
-                for (uint32_t r = 0; r < 16; r++) {
-                    const uint32_t mrow = mt * kGemmTile + out_row(i, r);
-                    const uint32_t ncol = nt * kGemmTile + out_col(jn);
-                    if (mrow < p.m && ncol < sg.rows) {
-                        const size_t o = (size_t)mrow * sg.ldy + ncol;
-                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][r] : acc[i][jn][r],
-                                                    sg.y + o);
-                    }
-                }
-        return;
-    }
-
-    // ---- split tile: publish this slice's partial ----
-    // Stored in the accumulator layout, float4 q of thread t (q = (i*2 + jn)*4
-    // + r/4) at (q*512 + t)*16 bytes of the slice's 256 KiB, so every store is
-    // a coalesced 16-byte access; gemm_reduce maps it back to (row, column).
-    const size_t slot = (size_t)(tile - p.split_tile0) * S + sl;
-    float4 *part = reinterpret_cast<float4 *>(p.ws + slot * kGemmTile * kGemmTile);
-#pragma unroll
-    for (uint32_t q = 0; q < 32; q++) {
-        const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
-        part[q * kGemmThreads + threadIdx.x] =
-            make_float4(acc[i][jn][4 * r4], acc[i][jn][4 * r4 + 1], acc[i][jn][4 * r4 + 2], acc[i][jn][4 * r4 + 3]);
-    }
-}
-
 // ---- the tail of a partial last round as 64x64 output tiles ----
 // When the tiles of the last round are few (at most one per 16 CUs), each
 // is cut into sixteen 64x64 output tiles, one workgroup per small tile.
@@ -435,9 +245,8 @@ constexpr uint32_t kTailLds = (kGemmThreads / 64) * kTailTile * kTailTile * 4;  
 static_assert(kTailLds <= 160 * 1024, "LDS");
 
 template <bool MULTI>
-__global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t tile = p.tail_tile0 + blockIdx.x / kTailPerTile, st = blockIdx.x % kTailPerTile;
+__device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uint8_t *lds) {
+    const uint32_t tile = p.tail_tile0 + idx / kTailPerTile, st = idx % kTailPerTile;
     const TileAt ta = tile_at<MULTI>(p, tile);
     const GemmSeg &sg = p.seg[ta.seg];
     const uint32_t row0 = ta.mt * kGemmTile + (st & 3) * kTailTile;    // token rows
@@ -566,6 +375,303 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     }
 }
 
+template <bool MULTI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    tail_tile<MULTI>(p, blockIdx.x, lds);
+}
+
+template <bool MULTI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
+    constexpr uint32_t kTM = 4, kTN = 2;   // 32x32 MFMA tiles per wavefront: 128 tokens x 64 rows
+    extern __shared__ __align__(16) uint8_t lds[];
+    lds_u8 *const ring = (lds_u8 *)lds;
+
+    const bool split = blockIdx.x >= p.split_tile0;
+    const uint32_t S = split ? p.nslices : 1;
+    const uint32_t u = split ? blockIdx.x - p.split_tile0 : 0;
+    const uint32_t tile = split ? p.split_tile0 + u / S : blockIdx.x;
+    const uint32_t sl = split ? u % S : 0;
+    const TileAt ta = tile_at<MULTI>(p, tile);
+    const GemmSeg &sg = p.seg[ta.seg];
+    const uint32_t mt = ta.mt, nt = ta.nt;
+    const uint32_t KB = p.kb;
+    const uint32_t kb0 = (sl * KB) / S, kb1 = ((sl + 1) * KB) / S;
+    const uint32_t st0 = 2 * kb0, st1 = 2 * kb1;   // stages of 64 columns
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wm = wv & 1, wn = wv >> 1;   // 2 x 4 wavefronts of 128 x 64
+
+    // ---- global sources of this wavefront's pieces ----
+    // A piece P (0..31): token rows (mt*8 + P/4)*32.., piece (h*4 + P%4) of the
+    // K block's eight (h = stage half); wavefront w copies 4w..4w+3.
+    // B piece Q (0..15): weight rows (nt*8 + Q/2)*32.., chunk 2h + Q%2;
+    // wavefront w copies 2w, 2w+1.  A missing second row group (odd NB)
+    // reads the last group instead; those columns are never stored.
+    const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb);
+    // Byte offsets (32-bit: the host keeps both operands under 4 GiB) that are
+    // wavefront-uniform, so they live in scalar registers; each copy adds the
+    // lane's 16 bytes and uses the global_load_lds saddr + voffset form.
+    uint32_t aoff[kALoads], boff[kBLoads];
+    const uint32_t lane16 = lane * 16;
+#pragma unroll
+    for (uint32_t i = 0; i < kALoads; i++) {
+        const uint32_t P = wv * kALoads + i;
+        aoff[i] = (mt * 8 + P / 4) * (KB * 8 * kChunkBytes) + (P % 4) * kChunkBytes;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBLoads; i++) {
+        const uint32_t Q = wv * kBLoads + i;
+        const uint32_t n32 = Q / 2;
+        const uint32_t nbk = min(nt * 2 + n32 / 4, sg.nb - 1);
+        boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
+    }
+    // Copy k of stage st into ring slot buf: k < kALoads an A piece, then the
+    // B pieces.
+    auto issue_piece = [&](uint32_t st, uint32_t buf, uint32_t k) {
+        const uint32_t kb = st >> 1, h = st & 1;
+        lds_u8 *la = ring + buf * kStageBytes;
+        if (k < kALoads) {
+            dma_1k(xa + (aoff[k] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
+                   la + (wv * kALoads + k) * kChunkBytes);
+        } else {
+            const uint32_t i = k - kALoads;
+            dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
+                   la + kStageA + (wv * kBLoads + i) * kChunkBytes);
+        }
+    };
+    auto issue = [&](uint32_t st, uint32_t buf) {
+#pragma unroll
+        for (uint32_t k = 0; k < kStageLoads; k++) issue_piece(st, buf, k);
+    };
+
+    // ---- block scales of the tile's two row groups, staged in LDS ----
+    // The loop takes them from registers (one K block per lane, refilled
+    // every 64 blocks), so no LDS read of a scale sits between its MFMAs and
+    // nothing waits for one there.  0 past the last row group.  Done before
+    // the first copy is issued, so this barrier drains nothing.
+    float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
+    for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
+        const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
+        const uint32_t nbg = nt * 2 + g;
+        float v = 0.0f;
+        if (nbg < sg.nb && kk < kb1 - kb0) v = sg.scale[(size_t)nbg * KB + kb0 + kk];
+        sc_lds[j] = v;
+    }
+    __syncthreads();
+    const float *my_sc = sc_lds + (wn >> 1) * kGemmMaxSliceKb - kb0;   // indexed by kb
+    uint32_t sc_base = kb0;                                           // lane i holds block sc_base + i
+    float sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
+    auto scale_of = [&](uint32_t kb) {   // kb in [sc_base, sc_base + 64)
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), kb - sc_base));
+    };
+
+    f32x16_t acc[kTM][kTN] = {};
+    float s_prev = 0.0f;
+
+    // Operands of one 32-column chunk: A for this wavefront's 4 token
+    // sub-tiles x 2 MFMA halves (bf16), B for its 2 weight sub-tiles (16 e4m3
+    // codes per lane, both halves).  Read from LDS one 1 KiB piece at a time.
+    struct Frags {
+        bf16x8_t a[kTM][2];
+        u32x4_t b[kTN];
+    };
+    constexpr uint32_t kPieces = 2 * kTM + kTN;   // 10
+    static_assert(kStageLoads + kPieces == 16, "one copy or read per MFMA of a phase");
+    auto read_a = [&](Frags &f, uint32_t buf, uint32_t jj, uint32_t i, uint32_t q) {
+        const uint8_t *la = lds + buf * kStageBytes;
+        f.a[i][q] = *reinterpret_cast<const bf16x8_t *>(la + (((wm * kTM + i) * 2 + jj) * 2 + q) * kChunkBytes +
+                                                        lane * 16);
+    };
+    auto read_b = [&](Frags &f, uint32_t buf, uint32_t jj, uint32_t jn) {
+        const uint8_t *la = lds + buf * kStageBytes;
+        f.b[jn] = *reinterpret_cast<const u32x4_t *>(la + kStageA + ((wn * kTN + jn) * 2 + jj) * kChunkBytes +
+                                                     lane * 16);
+    };
+    // ---- pipeline ----
+    // LDS ring of three stages (64 columns each, two per K block).  Stage s:
+    // its first chunk's operands are in registers (f0) when it starts; the
+    // second chunk's are read (f1) during the first chunk's MFMAs.  Then,
+    // once every wavefront has read all of stage s and stage s+1 has landed
+    // (one barrier), stage s+3 is copied into s's slot and stage s+1's first
+    // chunk is read during the second chunk's MFMAs.  Every wavefront issues
+    // exactly kStageLoads copies per stage (clamped to the last stage past
+    // the end), so "vmcnt <= kStageLoads" means: all but the newest stage
+    // have landed.
+    //
+    // Block scales: the accumulator is kept in units of the last live block
+    // scale.  Before the MFMAs of block kb+1 it is multiplied by r = s_prev /
+    // s_{kb+1}, after its last MFMA of block kb and before its first of block
+    // kb+1, so each accumulator sees the same products in the same order as
+    // with one multiply at the block boundary.  A block with scale 0 runs
+    // with keep = 0 and r = 1, so the accumulator keeps its units.  keep is
+    // the conversion's power-of-two scale: 1.0 (exact) for a live block, 0.0
+    // (= 2^-127) for a block whose scale is 0, which then adds at most
+    // 2^-127 * 448 * |x| per term (and NaN for a NaN code, as lut[code] * 0
+    // does).  No branches around the MFMAs.
+    issue(st0, 0);
+    issue(min(st0 + 1, st1 - 1), 1);
+    issue(min(st0 + 2, st1 - 1), 2);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
+    lds_barrier();
+    Frags f0, f1;
+    uint32_t buf = 0;
+    // B first, so the next phase's first B sub-tile can be converted
+    // while this phase's second half runs
+    read_b(f0, 0, 0, 0);
+    read_b(f0, 0, 0, 1);
+#pragma unroll
+    for (uint32_t k = 0; k < 2 * kTM; k++) read_a(f0, 0, 0, k >> 1, k & 1);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f0 and the first scales
+    const float sc0 = scale_of(kb0);
+    const bool live = sc0 != 0.0f;
+    float keep = live ? 1.0f : 0.0f;
+    float r = live ? 0.0f : 1.0f;            // the accumulator is still zero
+    s_prev = live ? sc0 : 0.0f;              // units of the accumulator after this block
+
+    // Each phase runs its 16 MFMAs accumulator by accumulator, both
+    // halves of a chunk back to back (slot t: accumulator a = t / 2,
+    // half q = t % 2; a = 4 jn + i, so B sub-tile 0 serves slots 0..7 and
+    // sub-tile 1 slots 8..15).  Beside MFMA t, pinned there
+    // (sched_barrier), at most one piece of each kind of other work:
+    //  - t < 8: one conversion of this phase's B sub-tile 1 (needed from
+    //    slot 8);  t >= 8: one conversion of the next phase's sub-tile 0
+    //    (needed at its slot 0; its LDS read was the phase's first);
+    //  - t < 10: the next phase's LDS reads (B sub-tiles, then A);
+    //    t >= 10 in a stage's second phase: the stage copies;
+    //  - in a K block's last phase and the next block's first, the
+    //    rescale plan's multiplies.
+    // No burst of VALU work holds back an MFMA: a wavefront's 16
+    // multiplies after one MFMA, or 8 conversions before one, delay its
+    // next MFMA by 30-60 cycles.
+    u32x4_t bw0[2], bw1[2];   // converted B sub-tiles 0 (this phase) and 1, halves q
+    auto cvt_part = [&](u32x4_t (&bw)[2], const u32x4_t &raw, uint32_t c, float kp) {
+        const uint32_t q = c >> 2, part = c & 3, w = raw[2 * q + (part >> 1)];
+        bw[q][part] = (part & 1) ? cvt_pk<true>(w, kp) : cvt_pk<false>(w, kp);
+    };
+#pragma unroll
+    for (uint32_t c = 0; c < 8; c++) cvt_part(bw0, f0.b[0], c, keep);
+    // phase: f = this phase's operands, fn = the next phase's (read into);
+    // g0 = rescale plan offset (0: last phase of a block, 16: first
+    // phase of a block, 32: none); second = the stage's second phase
+    // (copies of stage st_copy into ring slot cbuf).
+    auto phase = [&](const Frags &f, Frags &fn, uint32_t nbuf, uint32_t njj, float kp, float kp_next,
+                     auto g0c, float rr, auto secondc, uint32_t st_copy, uint32_t cbuf) {
+        constexpr uint32_t g0 = decltype(g0c)::value;
+        constexpr bool second = decltype(secondc)::value;
+        static_for<16>([&](auto tc) {
+            constexpr uint32_t t = decltype(tc)::value;
+            constexpr uint32_t a = t >> 1, q = t & 1, i = a & 3, jn = a >> 2;
+            if constexpr (jn == 0)
+                acc[i][0] = mfma32x32x16(f.a[i][q], __builtin_bit_cast(bf16x8_t, bw0[q]), acc[i][0]);
+            else
+                acc[i][1] = mfma32x32x16(f.a[i][q], __builtin_bit_cast(bf16x8_t, bw1[q]), acc[i][1]);
+            if constexpr (t < 8) {
+                cvt_part(bw1, f.b[1], t, kp);
+            } else {
+                if constexpr (t == 8) __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(7));   // fn.b[0]: read first
+                cvt_part(bw0, fn.b[0], t - 8, kp_next);
+            }
+            if constexpr (t < 2)
+                read_b(fn, nbuf, njj, t);
+            else if constexpr (t < kPieces)
+                read_a(fn, nbuf, njj, (t - 2) >> 1, t & 1);
+            else if constexpr (second)
+                issue_piece(st_copy, cbuf, t - kPieces);
+            if constexpr (g0 < 32) {
+                static_for<8>([&](auto acc_c) {
+                    constexpr uint32_t ac = decltype(acc_c)::value;
+                    constexpr uint32_t n = kRescale.cnt[g0 + t][ac], e0 = kRescale.first[g0 + t][ac];
+                    static_for<n>([&](auto ec) { acc[ac & 3][ac >> 2][e0 + decltype(ec)::value] *= rr; });
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    for (uint32_t kb = kb0; kb < kb1; kb++) {
+        if (kb + 1 == sc_base + 64) {
+            sc_base += 64;
+            sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        }
+        const bool live_n = kb + 1 < kb1 && scale_of(min(kb + 1, kb1 - 1)) != 0.0f;
+        const float sc_n = live_n ? scale_of(kb + 1) : 1.0f;
+        const float keep_n = live_n ? 1.0f : 0.0f;
+        const float r_n = live_n ? (s_prev != 0.0f ? s_prev / sc_n : 0.0f) : 1.0f;
+        const float s_prev_n = live_n ? sc_n : s_prev;
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<2>([&](auto hc) {
+            constexpr uint32_t h = decltype(hc)::value;
+            const uint32_t st = 2 * kb + h;
+            using G0a = std::integral_constant<uint32_t, h == 0 ? 16 : 32>;   // a block's first phase
+            using G0b = std::integral_constant<uint32_t, h == 1 ? 0 : 32>;    // a block's last phase
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f0 was read during the previous phase
+            phase(f0, f1, buf, 1, keep, keep, G0a{}, r, std::false_type{}, 0, 0);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // f1 is in registers: slot st is free
+            lds_barrier();
+            const uint32_t nb = buf == 2 ? 0 : buf + 1;
+            // past the end the reads of f0 are unused (in bounds)
+            phase(f1, f0, nb, 0, keep, h == 1 ? keep_n : keep, G0b{}, r_n, std::true_type{},
+                  min(st + 3, st1 - 1), buf);
+            buf = nb;
+        });
+        keep = keep_n;
+        r = r_n;
+        s_prev = s_prev_n;
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));   // no copy outlives the loop
+#pragma unroll
+    for (uint32_t i = 0; i < kTM; i++)
+#pragma unroll
+        for (uint32_t jn = 0; jn < kTN; jn++) acc[i][jn] *= s_prev;
+
+    // Output coordinates of accumulator element (i, jn, r) of this lane.
+    auto out_row = [&](uint32_t i, uint32_t r) -> uint32_t {
+        return wm * (32 * kTM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    };
+    auto out_col = [&](uint32_t jn) -> uint32_t { return wn * (32 * kTN) + jn * 32 + (lane & 31); };
+
+    if (!split) {
+#pragma unroll
+        for (uint32_t i = 0; i < kTM; i++)
+#pragma unroll
+            for (uint32_t jn = 0; jn < kTN; jn++)
+#pragma unroll
+                for (uint32_t r = 0; r < 16; r++) {
+                    const uint32_t mrow = mt * kGemmTile + out_row(i, r);
+                    const uint32_t ncol = nt * kGemmTile + out_col(jn);
+                    if (mrow < p.m && ncol < sg.rows) {
+                        const size_t o = (size_t)mrow * sg.ldy + ncol;
+                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][r] : acc[i][jn][r],
+                                                    sg.y + o);
+                    }
+                }
+        // One 64x64 tile of the last round's tail, while these stores drain
+        // (every workgroup reaches this point at about the same time, when
+        // the device's write bandwidth bounds the stores).
+        if (blockIdx.x < p.tail_fused) {
+            __syncthreads();   // the ring is free: every wavefront is past its last LDS read
+            tail_tile<MULTI>(p, blockIdx.x, lds);
+        }
+        return;
+    }
+
+    // ---- split tile: publish this slice's partial ----
+    // Stored in the accumulator layout, float4 q of thread t (q = (i*2 + jn)*4
+    // + r/4) at (q*512 + t)*16 bytes of the slice's 256 KiB, so every store is
+    // a coalesced 16-byte access; gemm_reduce maps it back to (row, column).
+    const size_t slot = (size_t)(tile - p.split_tile0) * S + sl;
+    float4 *part = reinterpret_cast<float4 *>(p.ws + slot * kGemmTile * kGemmTile);
+#pragma unroll
+    for (uint32_t q = 0; q < 32; q++) {
+        const uint32_t i = q / (4 * kTN), jn = (q / 4) % kTN, r4 = q & 3;
+        part[q * kGemmThreads + threadIdx.x] =
+            make_float4(acc[i][jn][4 * r4], acc[i][jn][4 * r4 + 1], acc[i][jn][4 * r4 + 2], acc[i][jn][4 * r4 + 3]);
+    }
+}
+
 // Ordered sum of the K slices of split tiles: y = ((p_0 + p_1) + p_2) + ...
 // One thread per float4 of a partial tile (16384 per tile); the layout is
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
@@ -663,6 +769,14 @@ hipError_t launch_act_to_bf16(const float *x, const float *x2, uint32_t ldx, uin
     return hipGetLastError();
 }
 
+static bool fuse_tail() {
+    static const bool on = [] {
+        const char *v = getenv("Q35MM_GEMM_FUSE_TAIL");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 template <bool MULTI>
 static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     static bool attr_set = false;
@@ -678,14 +792,17 @@ static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     const uint32_t tiles = p.mtiles * p.ntiles;
     const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
     const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
-    if (grid) hipLaunchKernelGGL(gemm_fp8_kernel<MULTI>, dim3(grid), dim3(kGemmThreads), kGemmLds, stream, p);
+    const uint32_t ntail = (tiles - p.tail_tile0) * kTailPerTile;   // 64x64 tiles
+    GemmParams q = p;
+    // the 64x64 tiles run in the whole-tile workgroups, after their stores
+    q.tail_fused = (ntail && !nsplit && p.split_tile0 >= ntail && fuse_tail()) ? ntail : 0;
+    if (grid) hipLaunchKernelGGL((gemm_fp8_kernel<MULTI>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
     if (nsplit) {
         const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
         hipLaunchKernelGGL(gemm_reduce_kernel<MULTI>, dim3(quads / 256), dim3(256), 0, stream, p);
     }
-    if (p.tail_tile0 < tiles)
-        hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3((tiles - p.tail_tile0) * kTailPerTile), dim3(kGemmThreads),
-                           kTailLds, stream, p);
+    if (ntail && !q.tail_fused)
+        hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3(ntail), dim3(kGemmThreads), kTailLds, stream, q);
     return hipGetLastError();
 }
 

@@ -175,6 +175,7 @@ struct GemmParams {
     uint32_t split_tile0;
     uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
     uint32_t tail_tile0; // first tile of the 64x64 tail (= mtiles * ntiles: none)
+    uint32_t tail_fused; // 64x64 tiles run by the first whole-tile workgroups after their own tile
 };
 
 struct GemmPlan {

@@ -122,6 +122,141 @@ __global__ __launch_bounds__(256) void mfma_rate(uint32_t iters, float *out, uin
     }
 }
 
+// ---- MFMA issue rate on data that changes -------------------------------------
+// As mfma_rate, but each MFMA takes one of 8 A and 8 B operand sets of
+// pseudo-random finite bf16 values (random signs, exponents within 2^-8..2^8,
+// random mantissas), so the matrix datapath toggles as it does on real
+// activations and weights.  The clock the chip holds then can lie well below
+// the one it holds on near-constant operands.
+template <bool E4M3B>
+__global__ __launch_bounds__(256) void mfma_rand(uint32_t iters, uint32_t seed, float *out, uint64_t *clocks) {
+    const uint32_t lane = threadIdx.x & 63;
+    u32x4 av[8], bv[8];
+    uint32_t h = seed ^ (blockIdx.x * 0x9e3779b9u) ^ (threadIdx.x * 0x85ebca6bu);
+    // wide: exponents 2^-8..2^7, 7 random mantissa bits; e4m3: a code's value
+    // (3 mantissa bits, exponents 2^-6..2^8) as the GEMM's widened weights are
+    auto rnd_bf16x2 = [&](bool e4m3) {
+        uint32_t r = 0;
+        for (int k = 0; k < 2; k++) {
+            h ^= h << 13; h ^= h >> 17; h ^= h << 5;
+            const uint32_t sign = (h >> 31) & 1, ex = (e4m3 ? 121 : 119) + ((h >> 20) & 15) % (e4m3 ? 15 : 16),
+                           man = e4m3 ? (h & 0x70) : (h & 127);
+            r |= ((sign << 15) | (ex << 7) | man) << (16 * k);
+        }
+        return r;
+    };
+    for (int c = 0; c < 8; c++)
+        for (int j = 0; j < 4; j++) {
+            av[c][j] = rnd_bf16x2(false);
+            bv[c][j] = rnd_bf16x2(E4M3B);
+        }
+    f32x16 acc[8] = {};
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[c]),
+                                                               __builtin_bit_cast(bf16x8, bv[(c + it) & 7]), acc[c], 0,
+                                                               0, 0);
+    }
+    __syncthreads();
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+    for (int c = 0; c < 8; c++) s += acc[c][lane & 15];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clocks[blockIdx.x * 2] = t1 - t0;
+        clocks[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
+// ---- MFMA issue rate with VALU work beside it ------------------------------
+// WPS wavefronts per SIMD, each running 8 accumulators of
+// v_mfma_f32_32x32x16_bf16 with, after every MFMA:
+//   MUL 1: two v_mul_f32 on an accumulator two MFMAs old (the GEMM's per-K-block
+//          rescale, spread evenly: 2 per MFMA);
+//   MUL 2: the same work in bursts: all 16 values of one accumulator after
+//          every eighth MFMA;
+//   CVT c: c v_cvt_scalef32_pk_bf16_fp8 building the B operand of the next
+//          group of four MFMAs (1 per MFMA = the GEMM's e4m3 -> bf16 widening
+//          for 128 x 64 wavefront tiles); CVT 8: eight after every eighth MFMA.
+// ORD 0 interleaves the accumulators (c = 0..7, each two MFMAs apart from
+// nothing it depends on); ORD 1 issues each accumulator's MFMAs in pairs
+// back to back (a dependent MFMA right after the one it accumulates onto).
+// Cycles are the workgroup's (barriers around the timed loop) per MFMA per
+// SIMD: 32 means the VALU work hides entirely.
+template <int WPS, int MUL, int CVT, int ORD>
+__global__ __launch_bounds__(256 * WPS, 2) void mfma_mix(uint32_t iters, float r, float *out, uint64_t *clocks) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t lane = threadIdx.x & 63;
+    bf16x8 a;
+    u32x4 bw[2];
+    for (int i = 0; i < 8; i++) a[i] = (__bf16)(float)((lane + i) & 7);
+    for (int j = 0; j < 4; j++) {
+        bw[0][j] = 0x3f803f80u + lane;
+        bw[1][j] = 0x3f803f80u + lane * 3;
+    }
+    const uint32_t codes = 0x38383838u ^ (lane << 8);
+    uint32_t side = 0;
+    f32x16 acc[8] = {};
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+        for (int u = 0; u < 8; u++)   // eight rounds unrolled: static element indices
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int ac = ORD ? ((c >> 1) + 4 * (u & 1)) : c;   // ORD 1: pairs on one accumulator
+                acc[ac] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, bw[c >> 2]),
+                                                                    acc[ac], 0, 0, 0);
+                if constexpr (MUL == 1) {
+                    const int e = (2 * u) & 15;
+                    const int t = ORD ? ((((c >> 1) + 2) & 3) + 4 * (u & 1)) : ((c + 6) & 7);
+                    acc[t][e] *= r;
+                    acc[t][e + 1] *= r;
+                } else if constexpr (MUL == 2) {
+                    if (c == 1) acc[ORD ? (3 + 4 * (u & 1)) : 7] *= r;
+                }
+                if constexpr (CVT == 8) {
+                    if (c == 1) {
+#pragma unroll
+                        for (int k = 0; k < 8; k++) {
+                            const uint32_t w = codes ^ (it * 64 + u * 8 + k);
+                            const bf16x2 v = (k & 1) ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                                                     : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+                            if (k < 4)
+                                bw[1][k] = __builtin_bit_cast(uint32_t, v);
+                            else
+                                side ^= __builtin_bit_cast(uint32_t, v);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < CVT; k++) {
+                        const uint32_t w = codes ^ (it * 64 + u * 8 + c);
+                        const bf16x2 v = (k & 1) ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                                                 : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+                        if (k == 0)
+                            bw[(c >> 2) ^ 1][c & 3] = __builtin_bit_cast(uint32_t, v);
+                        else
+                            side ^= __builtin_bit_cast(uint32_t, v);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+    __syncthreads();
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = (float)side;
+    for (int c = 0; c < 8; c++) s += acc[c][lane & 15];
+    out[blockIdx.x * 256 * WPS + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clocks[blockIdx.x * 2] = t1 - t0;
+        clocks[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
 // ---- LDS read rate -------------------------------------------------------
 __global__ __launch_bounds__(512) void lds_rate(uint32_t iters, float *out, uint64_t *clocks) {
     __shared__ __align__(16) uint8_t buf[64 * 1024];
@@ -228,6 +363,85 @@ static int run_mfma() {
     return 0;
 }
 
+template <int WPS, int MUL, int CVT, int ORD = 0>
+static void mix_case(float *out, uint64_t *clk) {
+    const uint32_t blocks = 256, iters = 256;   // x 64 MFMAs per wavefront
+    hipLaunchKernelGGL((mfma_mix<WPS, MUL, CVT, ORD>), dim3(blocks), dim3(256 * WPS), 0, 0, 8u, 0.999f, out, clk);
+    CK(hipDeviceSynchronize());
+    hipLaunchKernelGGL((mfma_mix<WPS, MUL, CVT, ORD>), dim3(blocks), dim3(256 * WPS), 0, 0, iters, 0.999f, out,
+                       clk);
+    CK(hipDeviceSynchronize());
+    std::vector<uint64_t> c(blocks * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    double cyc = 0;
+    for (uint32_t b = 0; b < blocks; b++) cyc += (double)c[2 * b];
+    cyc /= blocks;
+    printf("mix waves/SIMD %d  order %-11s  rescale %-6s  cvt %s:  %.1f cycles per MFMA per SIMD\n", WPS,
+           ORD ? "pairs" : "interleaved", MUL == 0 ? "none" : MUL == 1 ? "spread" : "burst",
+           CVT == 8 ? "burst 8/8" : CVT == 2 ? "2/MFMA" : CVT == 1 ? "1/MFMA" : "none",
+           cyc / (iters * 64.0 * WPS));
+}
+
+static int run_mix() {
+    float *out;
+    uint64_t *clk;
+    CK(hipMalloc(&out, 256 * 512 * sizeof(float)));
+    CK(hipMalloc(&clk, 256 * 2 * sizeof(uint64_t)));
+    mix_case<1, 0, 0>(out, clk);
+    mix_case<1, 1, 0>(out, clk);
+    mix_case<1, 2, 0>(out, clk);
+    mix_case<1, 0, 1>(out, clk);
+    mix_case<1, 0, 8>(out, clk);
+    mix_case<1, 1, 1>(out, clk);
+    mix_case<1, 2, 8>(out, clk);
+    mix_case<1, 0, 0, 1>(out, clk);
+    mix_case<1, 1, 1, 1>(out, clk);
+    mix_case<2, 0, 0>(out, clk);
+    mix_case<2, 1, 0>(out, clk);
+    mix_case<2, 2, 0>(out, clk);
+    mix_case<2, 0, 1>(out, clk);
+    mix_case<2, 0, 8>(out, clk);
+    mix_case<2, 1, 1>(out, clk);
+    mix_case<2, 2, 8>(out, clk);
+    mix_case<2, 0, 0, 1>(out, clk);
+    mix_case<2, 1, 1, 1>(out, clk);
+    return 0;
+}
+
+static int run_mfma_rand() {
+    const uint32_t blocks = 256;
+    float *out;
+    uint64_t *clk;
+    CK(hipMalloc(&out, blocks * 256 * sizeof(float)));
+    CK(hipMalloc(&clk, blocks * 2 * sizeof(uint64_t)));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    for (int e4m3 = 0; e4m3 < 2; e4m3++)
+    for (uint32_t iters : {4096u, 65536u}) {   // ~0.6 ms and ~10 ms of MFMAs
+        auto kern = e4m3 ? mfma_rand<true> : mfma_rand<false>;
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, 0, 64u, 1u, out, clk);
+        CK(hipDeviceSynchronize());
+        CK(hipEventRecord(e0));
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, 0, iters, 7u, out, clk);
+        CK(hipEventRecord(e1));
+        CK(hipEventSynchronize(e1));
+        const double sec = time_ms(e0, e1) * 1e-3;
+        std::vector<uint64_t> c(blocks * 2);
+        CK(hipMemcpy(c.data(), clk, c.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+        double cyc = 0, real = 0;
+        for (uint32_t b = 0; b < blocks; b++) {
+            cyc += (double)c[2 * b];
+            real += (double)c[2 * b + 1];
+        }
+        const double flops = (double)blocks * 4 * iters * 8 * 32 * 32 * 16 * 2;
+        printf("mfma 32x32x16 bf16, random A, %s B: %.1f TFLOP/s over %.3f ms; core clock %.2f GHz; "
+               "%.1f cycles per MFMA per SIMD\n", e4m3 ? "e4m3-valued" : "random",
+               flops / sec / 1e12, sec * 1e3, cyc / real * 0.1, cyc / blocks / (iters * 8.0));
+    }
+    return 0;
+}
+
 static int run_lds() {
     const uint32_t blocks = 256, iters = 4096;
     float *out;
@@ -257,6 +471,8 @@ int main(int argc, char **argv) {
     if (argc >= 2 && !strcmp(argv[1], "read")) return run_read(argc >= 3 ? strtoul(argv[2], nullptr, 10) : 1536);
     if (argc >= 2 && !strcmp(argv[1], "mfma")) return run_mfma();
     if (argc >= 2 && !strcmp(argv[1], "lds")) return run_lds();
-    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma\n", argv[0]);
+    if (argc >= 2 && !strcmp(argv[1], "mix")) return run_mix();
+    if (argc >= 2 && !strcmp(argv[1], "mfma_rand")) return run_mfma_rand();
+    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma | mfma_rand | mix\n", argv[0]);
     return 2;
 }
