@@ -380,7 +380,7 @@ def bench_host_abi(q, wl, calls=200):
         out[name] = {"us_per_call": round(us, 2), "calls": calls}
         q.release(W)
     out["note"] = ("q35_mm_fp8 on host pointers, weight already resident: fingerprint check, x copied in, "
-                   "GEMV, y copied out, stream synchronised; includes the ctypes call")
+                   "GEMV, completion flag waited for, y copied out; includes the ctypes call")
     return out
 
 

@@ -152,6 +152,21 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(const float *__restrict__
     for (size_t i = 4 * n4 + i0; i < n; i += stride) dst[i] = src[i];
 }
 
+// Completion flag of a host-pointer call: runs after the call's kernels on
+// the same stream (so after their completion and end-of-kernel release) and
+// stores v into pinned host memory, where the calling thread waits for it.
+__global__ __launch_bounds__(64) void done_flag_kernel(uint32_t *flag, uint32_t v) {
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+hipError_t launch_done_flag(uint32_t *flag, uint32_t v, hipStream_t stream) {
+    hipLaunchKernelGGL(done_flag_kernel, dim3(1), dim3(64), 0, stream, flag, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy_f32(const float *src, float *dst, size_t n, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>(64, (n + 4095) / 4096);

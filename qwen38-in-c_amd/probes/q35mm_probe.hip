@@ -25,9 +25,28 @@
 //     accumulator chains of back-to-back MFMAs; also the core clock under
 //     that load (s_memtime ticks against s_memrealtime's 100 MHz).  Prints
 //     TFLOP/s and cycles per MFMA.
+//
+//   q35mm_probe mfma_rand | mfma_order
+//     The same on operands that change like real activations and weights
+//     (mfma_order: the prefill GEMM's 4 x 2 tile pattern in three issue
+//     orders, one or two wavefronts per SIMD).
+//
+//   q35mm_probe mix
+//     MFMA issue with VALU work (rescale multiplies, e4m3 conversions)
+//     beside it, spread or in bursts.
+//
+//   q35mm_probe launch
+//     Cost of one more launch in a sequence of dependent launches (empty
+//     kernel, on a stream and as a graph).
+//
+//   q35mm_probe sync [spin]
+//     Host round trip of launch + wait: hipStreamSynchronize,
+//     hipEventSynchronize, or spinning on a flag the kernel stores into
+//     pinned memory (spin: hipDeviceScheduleSpin first).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -71,6 +90,44 @@ __global__ __launch_bounds__(256) void read_tiles(const uint8_t *codes, uint32_t
             }
     }
     if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+}
+
+// ---- read: S sub-tiles per workgroup, W wavefronts splitting K -------------------
+// S = 2: 64 rows per workgroup, S = 4: a whole 128-row group (16 KiB per K
+// block).  SM: the weight as if stored sub-tile-major (each 32-row
+// sub-tile's K blocks contiguous, 4 KiB apart) instead of block-major.
+template <int D, int S, int W, bool SM>
+__global__ __launch_bounds__(64 * W) void read_group(const uint8_t *codes, uint32_t kb, float *out) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t sub0 = blockIdx.x * S;
+    const uint32_t k0 = wv * kb / W, n = (wv + 1) * kb / W - k0;
+    auto addr = [&](uint32_t s, uint32_t k, uint32_t j) -> const u32x4 * {
+        const uint32_t sub = sub0 + s, g = sub >> 2, t = sub & 3;
+        const size_t o = SM ? ((size_t)sub * kb + k) * 4096 : ((size_t)g * kb * 4 + (size_t)k * 4 + t) * 4096;
+        return (const u32x4 *)(codes + o + j * 1024 + lane * 16);
+    };
+    uint32_t acc = 0;
+    if (n) {
+        u32x4 buf[D][S][4];
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int s = 0; s < S; s++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) buf[d][s][j] = __builtin_nontemporal_load(addr(s, k0 + min((uint32_t)d, n - 1), j));
+        for (uint32_t i = 0; i < n; i += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++)
+#pragma unroll
+                for (int s = 0; s < S; s++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (i + d < n) acc += buf[d][s][j].x ^ buf[d][s][j].w;
+                        buf[d][s][j] = __builtin_nontemporal_load(addr(s, k0 + min(i + d + D, n - 1), j));
+                    }
+        }
+    }
+    if (lane == 0) out[blockIdx.x * W + wv] = (float)acc;
 }
 
 // ---- read: one contiguous stream -------------------------------------------
@@ -153,12 +210,17 @@ __global__ __launch_bounds__(256) void mfma_rand(uint32_t iters, uint32_t seed, 
     f32x16 acc[8] = {};
     __syncthreads();
     const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
-    for (uint32_t it = 0; it < iters; it++) {
+    // eight iterations per trip (iters is a multiple of 8), so every operand
+    // index is a compile-time constant: a B index depending on the loop
+    // counter compiles to s_set_gpr_idx and four v_mov per MFMA
+    for (uint32_t it = 0; it < iters; it += 8) {
 #pragma unroll
-        for (int c = 0; c < 8; c++)
-            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[c]),
-                                                               __builtin_bit_cast(bf16x8, bv[(c + it) & 7]), acc[c], 0,
-                                                               0, 0);
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[c]),
+                                                                   __builtin_bit_cast(bf16x8, bv[(c + u) & 7]), acc[c],
+                                                                   0, 0, 0);
     }
     __syncthreads();
     const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
@@ -169,6 +231,75 @@ __global__ __launch_bounds__(256) void mfma_rand(uint32_t iters, uint32_t seed, 
         clocks[blockIdx.x * 2] = t1 - t0;
         clocks[blockIdx.x * 2 + 1] = r1 - r0;
     }
+}
+
+// ---- MFMA issue order on operands that change (mfma_order) ----------------
+// The prefill GEMM's operand pattern for one 32-column chunk of a 128 x 64
+// wavefront tile: A tiles i < 4 and B tiles jn < 2, each in two k-halves q,
+// 16 MFMAs on 8 accumulators (acc[4*jn + i] += A[i][q] * B[jn][q]).  Two
+// operand sets of random bf16 A and e4m3-valued B alternate chunk by chunk.
+// ORD 0 "pairs": accumulator by accumulator, both halves back to back
+//   (A and B change at every MFMA);
+// ORD 1 "b-hold": q, then jn, then i (B held for four MFMAs, A changes);
+// ORD 2 "a-hold": q, then i, then jn (A held for two MFMAs, B alternates).
+// Bit-identical orders for the GEMM: each accumulator still adds half 0,
+// then half 1.
+template <int ORD, int WPS>
+__global__ __launch_bounds__(256 * WPS) void mfma_order(uint32_t iters, uint32_t seed, float *out, uint64_t *clocks) {
+    const uint32_t lane = threadIdx.x & 63;
+    u32x4 av[2][4][2], bv[2][2][2];
+    uint32_t h = seed ^ (blockIdx.x * 0x9e3779b9u) ^ (threadIdx.x * 0x85ebca6bu);
+    auto rnd_bf16x2 = [&](bool e4m3) {
+        uint32_t r = 0;
+        for (int k = 0; k < 2; k++) {
+            h ^= h << 13; h ^= h >> 17; h ^= h << 5;
+            const uint32_t sign = (h >> 31) & 1, ex = (e4m3 ? 121 : 119) + ((h >> 20) & 15) % (e4m3 ? 15 : 16),
+                           man = e4m3 ? (h & 0x70) : (h & 127);
+            r |= ((sign << 15) | (ex << 7) | man) << (16 * k);
+        }
+        return r;
+    };
+    for (int st = 0; st < 2; st++)
+        for (int q = 0; q < 2; q++)
+            for (int j = 0; j < 4; j++) {
+                for (int i = 0; i < 4; i++) av[st][i][q][j] = rnd_bf16x2(false);
+                for (int jn = 0; jn < 2; jn++) bv[st][jn][q][j] = rnd_bf16x2(true);
+            }
+    f32x16 acc[8] = {};
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; it += 2) {
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+            for (int t = 0; t < 16; t++) {
+                int i, jn, q;
+                if (ORD == 0) { const int a = t >> 1; q = t & 1; i = a & 3; jn = a >> 2; }
+                else if (ORD == 1) { q = t >> 3; jn = (t >> 2) & 1; i = t & 3; }
+                else { q = t >> 3; i = (t >> 1) & 3; jn = t & 1; }
+                acc[4 * jn + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, av[st][i][q]), __builtin_bit_cast(bf16x8, bv[st][jn][q]),
+                    acc[4 * jn + i], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);   // keep the order as written
+            }
+    }
+    __syncthreads();
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+    for (int c = 0; c < 8; c++) s += acc[c][lane & 15];
+    out[blockIdx.x * 256 * WPS + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clocks[blockIdx.x * 2] = t1 - t0;
+        clocks[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
+// ---- launch gap (launch) -----------------------------------------------------
+// Back-to-back launches of a kernel that does nothing (one store per
+// workgroup, so it is not optimised away), on one stream and as a captured
+// graph: what one more launch in a sequence of dependent launches costs.
+__global__ __launch_bounds__(256) void empty_kernel(float *out) {
+    if (threadIdx.x == 0 && out) out[blockIdx.x] = 0.0f;
 }
 
 // ---- MFMA issue rate with VALU work beside it ------------------------------
@@ -298,6 +429,8 @@ static int run_read(size_t pool_mb) {
     hipEvent_t e0, e1;
     CK(hipEventCreate(&e0));
     CK(hipEventCreate(&e1));
+    hipStream_t gst;
+    CK(hipStreamCreate(&gst));
     for (const Shape &sh : shapes) {
         const uint32_t nb = (sh.n + 127) / 128, kb = (sh.k + 127) / 128;
         const size_t bytes = (size_t)nb * kb * 16384;
@@ -306,13 +439,23 @@ static int run_read(size_t pool_mb) {
         CK(hipMalloc(&pool, bytes * copies));
         CK(hipMemset(pool, 0x35, bytes * copies));
         const uint32_t subs = (sh.n + 31) / 32;
-        for (int variant = 0; variant < 3; variant++) {
-            auto launch = [&](int i) {
+        static const char *const vname[] = {"tiles/2", "tiles/3", "linear", "sm/2", "g2w4/2", "g2w8/2", "g4w8/2",
+                                            "g4w16/2", "g2w4sm/2"};
+        for (int variant = 0; variant < 9; variant++) {
+            if (variant >= 4 && subs % 4) continue;
+            auto launch_on = [&](int i, hipStream_t s) {
                 const uint8_t *c = pool + (size_t)(i % copies) * bytes;
-                if (variant == 0) hipLaunchKernelGGL(read_tiles<2>, dim3(subs), dim3(256), 0, 0, c, kb, out);
-                else if (variant == 1) hipLaunchKernelGGL(read_tiles<3>, dim3(subs), dim3(256), 0, 0, c, kb, out);
-                else hipLaunchKernelGGL(read_linear, dim3(256), dim3(256), 0, 0, c, bytes, out);
+                if (variant == 0) hipLaunchKernelGGL(read_tiles<2>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else if (variant == 1) hipLaunchKernelGGL(read_tiles<3>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else if (variant == 2) hipLaunchKernelGGL(read_linear, dim3(256), dim3(256), 0, s, c, bytes, out);
+                else if (variant == 3) hipLaunchKernelGGL((read_group<2, 1, 4, true>), dim3(subs), dim3(256), 0, s, c, kb, out);
+                else if (variant == 4) hipLaunchKernelGGL((read_group<2, 2, 4, false>), dim3(subs / 2), dim3(256), 0, s, c, kb, out);
+                else if (variant == 5) hipLaunchKernelGGL((read_group<2, 2, 8, false>), dim3(subs / 2), dim3(512), 0, s, c, kb, out);
+                else if (variant == 6) hipLaunchKernelGGL((read_group<2, 4, 8, false>), dim3(subs / 4), dim3(512), 0, s, c, kb, out);
+                else if (variant == 7) hipLaunchKernelGGL((read_group<2, 4, 16, false>), dim3(subs / 4), dim3(1024), 0, s, c, kb, out);
+                else hipLaunchKernelGGL((read_group<2, 2, 4, true>), dim3(subs / 2), dim3(256), 0, s, c, kb, out);
             };
+            auto launch = [&](int i) { launch_on(i, 0); };
             for (int i = 0; i < 8; i++) launch(i);
             CK(hipDeviceSynchronize());
             const int reps = 200;
@@ -321,9 +464,26 @@ static int run_read(size_t pool_mb) {
             CK(hipEventRecord(e1));
             CK(hipEventSynchronize(e1));
             const double us = time_ms(e0, e1) * 1e3 / reps;
-            printf("read %-22s %-8s %8.2f us %7.0f GB/s (%zu bytes, %d copies)\n", sh.name,
-                   variant == 0 ? "tiles/2" : variant == 1 ? "tiles/3" : "linear", us, bytes / us / 1e3, bytes,
-                   copies);
+            // the same launches captured once and replayed as a graph (as the
+            // benchmark launches its kernels): each launch costs less there
+            hipGraph_t g;
+            hipGraphExec_t ge;
+            CK(hipStreamBeginCapture(gst, hipStreamCaptureModeGlobal));
+            for (int i = 0; i < reps; i++) launch_on(i, gst);
+            CK(hipStreamEndCapture(gst, &g));
+            CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+            CK(hipGraphLaunch(ge, gst));
+            CK(hipStreamSynchronize(gst));
+            CK(hipEventRecord(e0, gst));
+            CK(hipGraphLaunch(ge, gst));
+            CK(hipEventRecord(e1, gst));
+            CK(hipEventSynchronize(e1));
+            const double us_g = time_ms(e0, e1) * 1e3 / reps;
+            CK(hipGraphExecDestroy(ge));
+            CK(hipGraphDestroy(g));
+            printf("read %-22s %-8s %8.2f us %7.0f GB/s; graph %8.2f us %7.0f GB/s (%zu bytes, %d copies)\n",
+                   sh.name, vname[variant], us, bytes / us / 1e3,
+                   us_g, bytes / us_g / 1e3, bytes, copies);
             fflush(stdout);
         }
         CK(hipFree(pool));
@@ -442,6 +602,142 @@ static int run_mfma_rand() {
     return 0;
 }
 
+template <int ORD, int WPS>
+static void order_case(float *out, uint64_t *clk, hipEvent_t e0, hipEvent_t e1, uint32_t iters) {
+    const uint32_t blocks = 256;
+    hipLaunchKernelGGL((mfma_order<ORD, WPS>), dim3(blocks), dim3(256 * WPS), 0, 0, 64u, 1u, out, clk);
+    CK(hipDeviceSynchronize());
+    CK(hipEventRecord(e0));
+    hipLaunchKernelGGL((mfma_order<ORD, WPS>), dim3(blocks), dim3(256 * WPS), 0, 0, iters, 7u, out, clk);
+    CK(hipEventRecord(e1));
+    CK(hipEventSynchronize(e1));
+    const double sec = time_ms(e0, e1) * 1e-3;
+    std::vector<uint64_t> c(blocks * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    double cyc = 0, real = 0;
+    for (uint32_t b = 0; b < blocks; b++) {
+        cyc += (double)c[2 * b];
+        real += (double)c[2 * b + 1];
+    }
+    const double mfmas_per_simd = (double)iters * 16 * WPS;
+    const double flops = (double)blocks * 4 * mfmas_per_simd * 32 * 32 * 16 * 2;
+    printf("mfma order %-11s waves/SIMD %d: %.1f TFLOP/s over %.3f ms; core clock %.2f GHz; %.1f cycles per MFMA "
+           "per SIMD\n", ORD == 0 ? "pairs" : ORD == 1 ? "b-hold" : "a-hold", WPS, flops / sec / 1e12, sec * 1e3,
+           cyc / real * 0.1, cyc / blocks / mfmas_per_simd);
+    fflush(stdout);
+}
+
+static int run_mfma_order() {
+    float *out;
+    uint64_t *clk;
+    CK(hipMalloc(&out, 256 * 512 * sizeof(float)));
+    CK(hipMalloc(&clk, 256 * 2 * sizeof(uint64_t)));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    for (uint32_t iters : {4096u, 32768u}) {   // x 16 MFMAs per wavefront: ~0.6 ms and ~5 ms
+        order_case<0, 1>(out, clk, e0, e1, iters);
+        order_case<1, 1>(out, clk, e0, e1, iters);
+        order_case<2, 1>(out, clk, e0, e1, iters);
+        order_case<0, 2>(out, clk, e0, e1, iters / 2);
+        order_case<1, 2>(out, clk, e0, e1, iters / 2);
+        order_case<2, 2>(out, clk, e0, e1, iters / 2);
+    }
+    return 0;
+}
+
+static int run_launch() {
+    float *out;
+    CK(hipMalloc(&out, 4096 * sizeof(float)));
+    hipStream_t st;
+    CK(hipStreamCreate(&st));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    const int n = 400;
+    for (uint32_t blocks : {1u, 256u, 1024u}) {
+        for (int i = 0; i < 20; i++) hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(256), 0, st, out);
+        CK(hipStreamSynchronize(st));
+        CK(hipEventRecord(e0, st));
+        for (int i = 0; i < n; i++) hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(256), 0, st, out);
+        CK(hipEventRecord(e1, st));
+        CK(hipEventSynchronize(e1));
+        const double us_stream = time_ms(e0, e1) * 1e3 / n;
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+        for (int i = 0; i < n; i++) hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(256), 0, st, out);
+        CK(hipStreamEndCapture(st, &g));
+        CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        CK(hipGraphLaunch(ge, st));
+        CK(hipStreamSynchronize(st));
+        CK(hipEventRecord(e0, st));
+        CK(hipGraphLaunch(ge, st));
+        CK(hipEventRecord(e1, st));
+        CK(hipEventSynchronize(e1));
+        const double us_graph = time_ms(e0, e1) * 1e3 / n;
+        printf("launch empty kernel, %4u workgroups: %.2f us per launch on a stream, %.2f us in a graph\n", blocks,
+               us_stream, us_graph);
+        fflush(stdout);
+        CK(hipGraphExecDestroy(ge));
+        CK(hipGraphDestroy(g));
+    }
+    return 0;
+}
+
+// Host round trip of one launch: launch, then wait for it on the host, as a
+// synchronous library call does.  "sync": hipStreamSynchronize; "event":
+// hipEventSynchronize on an event recorded after the launch; "flag": the
+// kernel's last store goes to pinned host memory and the host spins on it.
+__global__ __launch_bounds__(64) void flag_kernel(volatile uint32_t *flag, uint32_t v) {
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        *flag = v;
+    }
+}
+
+static int run_sync(bool spin) {
+    if (spin) CK(hipSetDeviceFlags(hipDeviceScheduleSpin));
+    hipStream_t st;
+    CK(hipStreamCreate(&st));
+    float *out;
+    CK(hipMalloc(&out, 4096 * sizeof(float)));
+    uint32_t *flag;
+    CK(hipHostMalloc(&flag, 64, hipHostMallocDefault));
+    *flag = 0;
+    hipEvent_t ev;
+    CK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    const int n = 2000;
+    for (int mode = 0; mode < 3; mode++) {
+        double best = 1e30;
+        for (int rep = 0; rep < 3; rep++) {
+            auto t0 = std::chrono::steady_clock::now();
+            for (int i = 0; i < n; i++) {
+                if (mode == 2) {
+                    const uint32_t v = (uint32_t)(rep * n + i + 1);
+                    hipLaunchKernelGGL(flag_kernel, dim3(1), dim3(64), 0, st, (volatile uint32_t *)flag, v);
+                    while (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != v) __builtin_ia32_pause();
+                } else {
+                    hipLaunchKernelGGL(empty_kernel, dim3(160), dim3(256), 0, st, out);
+                    if (mode == 0) {
+                        CK(hipStreamSynchronize(st));
+                    } else {
+                        CK(hipEventRecord(ev, st));
+                        CK(hipEventSynchronize(ev));
+                    }
+                }
+            }
+            CK(hipStreamSynchronize(st));
+            const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() / n;
+            best = std::min(best, us);
+        }
+        printf("host round trip (%s scheduling), launch + %s: %.2f us\n", spin ? "spin" : "default",
+               mode == 0 ? "hipStreamSynchronize" : mode == 1 ? "hipEventSynchronize" : "spin on a pinned flag", best);
+        fflush(stdout);
+    }
+    return 0;
+}
+
 static int run_lds() {
     const uint32_t blocks = 256, iters = 4096;
     float *out;
@@ -473,6 +769,9 @@ int main(int argc, char **argv) {
     if (argc >= 2 && !strcmp(argv[1], "lds")) return run_lds();
     if (argc >= 2 && !strcmp(argv[1], "mix")) return run_mix();
     if (argc >= 2 && !strcmp(argv[1], "mfma_rand")) return run_mfma_rand();
-    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma | mfma_rand | mix\n", argv[0]);
+    if (argc >= 2 && !strcmp(argv[1], "mfma_order")) return run_mfma_order();
+    if (argc >= 2 && !strcmp(argv[1], "launch")) return run_launch();
+    if (argc >= 2 && !strcmp(argv[1], "sync")) return run_sync(argc >= 3 && !strcmp(argv[2], "spin"));
+    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma | mfma_rand | mfma_order | mix | launch | sync [spin]\n", argv[0]);
     return 2;
 }
