@@ -154,18 +154,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
     for (uint32_t i = 1; i < 4; i++)
         if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
     const GemvSeg &sg = p.seg[si];
-    // Rows [r0, r1) of the segment: unit_rows rows per workgroup, or quads
-    // [c*Q/P, (c+1)*Q/P) of its Q quads over its P workgroups (the host keeps
-    // P <= Q and ceil(Q/P) <= 8).
+    // Rows [r0, r1) of the segment: unit_rows rows per workgroup, or its Q
+    // quads over its P workgroups, qbase = Q / P quads each and one more for
+    // the first qrem = Q % P (the host keeps P <= Q and ceil(Q/P) <= 8).
+    // No division here: every instruction a launch executes is fetched into
+    // an instruction cache that starts cold at each launch (about 0.4 ns
+    // per byte of code on this part), and a 64-bit division is ~800 bytes.
     const uint32_t c = blockIdx.x - sg.cta_begin;
     uint32_t r0, r1;
     if (sg.unit_rows) {
         r0 = c * sg.unit_rows;
         r1 = min(r0 + sg.unit_rows, sg.rows);
     } else {
-        const uint32_t Q = (sg.rows + 3) >> 2, P = sg.nctas;
-        r0 = 4 * (uint32_t)((uint64_t)c * Q / P);
-        r1 = min(4 * (uint32_t)((uint64_t)(c + 1) * Q / P), sg.rows);
+        r0 = 4 * (c * sg.qbase + min(c, sg.qrem));
+        r1 = min(4 * ((c + 1) * sg.qbase + min(c + 1, sg.qrem)), sg.rows);
     }
     const uint32_t KB = p.kb, M = p.m, R = stage_rows(M);
 
@@ -325,12 +327,19 @@ RowsKernel rows_kernel(uint32_t depth, uint32_t vec_mt) {
 }
 }  // namespace
 
-hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, uint32_t waves, uint32_t depth, hipStream_t stream) {
+hipError_t launch_gemv_rows(const GemvParams &pin, uint32_t cus, uint32_t waves, uint32_t depth,
+                            hipStream_t stream) {
+    GemvParams p = pin;
     if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || (waves != 4 && waves != 8) ||
         !gemv_rows_shape(p.kb, waves) || p.nseg == 0 || p.nseg > 4)
         return hipErrorInvalidValue;
     for (uint32_t s = 0; s < p.nseg; s++) {
-        const GemvSeg &g = p.seg[s];
+        GemvSeg &g = p.seg[s];
+        if (!g.unit_rows && g.nctas) {
+            const uint32_t q = (g.rows + 3) / 4;
+            g.qbase = q / g.nctas;
+            g.qrem = q % g.nctas;
+        }
         const uint32_t q = (g.rows + 3) / 4;
         const bool ok = g.unit_rows ? g.unit_rows <= kSubRows && (uint64_t)g.nctas * g.unit_rows >= g.rows &&
                                           (uint64_t)(g.nctas - 1) * g.unit_rows < g.rows

@@ -59,6 +59,8 @@ struct GemvSeg {
     uint32_t ws_off;     // float offset of the segment's partials [nb][maxc][8][128]
     uint32_t cnt_off;    // offset of the segment's arrival counters [nb]
     uint32_t unit_rows;  // row-split GEMV: rows per workgroup (0: balanced 4-row quads)
+    uint32_t qbase;      // row-split quads: every range holds qbase quads,
+    uint32_t qrem;       //   the first qrem ranges one more (set by launch_gemv_rows)
 };
 
 // What the staged activations are, per column k of token t:

@@ -92,6 +92,74 @@ __global__ __launch_bounds__(256) void read_tiles(const uint8_t *codes, uint32_t
     if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
 }
 
+// read_tiles<2> behind NOPS s_nop instructions before the first load: what
+// a longer stretch of code at the start of a kernel costs (at one
+// instruction per cycle, 1600 s_nop take 0.8 us; more means the code is
+// fetched cold).
+template <int NOPS>
+__global__ __launch_bounds__(256) void read_tiles_pad(const uint8_t *codes, uint32_t kb, float *out) {
+    if constexpr (NOPS == 400) asm volatile(".rept 400\n s_nop 0\n .endr");
+    if constexpr (NOPS == 1600) asm volatile(".rept 1600\n s_nop 0\n .endr");
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t sub = blockIdx.x, g = sub >> 2, s = sub & 3;
+    const uint32_t k0 = wv * kb / 4, n = (wv + 1) * kb / 4 - k0;
+    const uint8_t *b = codes + ((size_t)g * kb * 4 + s) * 4096 + (size_t)k0 * 16384 + lane * 16;
+    u32x4 buf[2][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min((uint32_t)d, n - 1) * 16384 + j * 1024));
+    for (uint32_t i = 0; i < n; i += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; d++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (i + d < n) acc += buf[d][j].x ^ buf[d][j].w;
+                buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min(i + d + 2, n - 1) * 16384 + j * 1024));
+            }
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+}
+
+// read_tiles with timestamps (s_memrealtime, 100 MHz): entry, first block
+// consumed, end; wavefront 0 of each workgroup writes them to st[3 * wg].
+template <int D>
+__global__ __launch_bounds__(256) void read_tiles_st(const uint8_t *codes, uint32_t kb, float *out, uint32_t *st) {
+    const uint32_t t0 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    uint32_t t1 = 0;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t sub = blockIdx.x, g = sub >> 2, s = sub & 3;
+    const uint32_t k0 = wv * kb / 4, n = (wv + 1) * kb / 4 - k0;
+    const uint8_t *b = codes + ((size_t)g * kb * 4 + s) * 4096 + (size_t)k0 * 16384 + lane * 16;
+    u32x4 buf[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int d = 0; d < D; d++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min((uint32_t)d, n - 1) * 16384 + j * 1024));
+    for (uint32_t i = 0; i < n; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (i + d < n) acc += buf[d][j].x ^ buf[d][j].w;
+                buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min(i + d + D, n - 1) * 16384 + j * 1024));
+            }
+            if (i + d == 0) t1 = (uint32_t)__builtin_amdgcn_s_memrealtime() + (acc & 1) * 0;
+        }
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+    const uint32_t t2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    if (wv == 0 && lane == 0) {
+        st[3 * blockIdx.x] = t0;
+        st[3 * blockIdx.x + 1] = t1;
+        st[3 * blockIdx.x + 2] = t2;
+    }
+}
+
 // ---- read: S sub-tiles per workgroup, W wavefronts splitting K -------------------
 // S = 2: 64 rows per workgroup, S = 4: a whole 128-row group (16 KiB per K
 // block).  SM: the weight as if stored sub-tile-major (each 32-row
@@ -128,6 +196,34 @@ __global__ __launch_bounds__(64 * W) void read_group(const uint8_t *codes, uint3
         }
     }
     if (lane == 0) out[blockIdx.x * W + wv] = (float)acc;
+}
+
+// ---- decode layer step of raw reads, with the next weight's first blocks
+// fetched ahead on a second stream (step) ------------------------------------
+// prefetch_head<D>: for every 32-row sub-tile and each of the four
+// wavefront K ranges of the row-split decomposition, the first D K blocks
+// (what a read_tiles launch on the same weight loads first), with plain
+// loads so they stay in the caches; grid-stride over (sub-tile, range).
+template <int D>
+__global__ __launch_bounds__(256) void prefetch_head(const uint8_t *codes, uint32_t kb, uint32_t subs, float *out) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t acc = 0;
+    for (uint32_t u = blockIdx.x * 4 + wv; u < subs * 4; u += gridDim.x * 4) {
+        const uint32_t sub = u >> 2, w = u & 3, g = sub >> 2, t = sub & 3;
+        const uint32_t k0 = w * kb / 4, n = (w + 1) * kb / 4 - k0;
+        u32x4 v[D][4];
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[d][j] = *(const u32x4 *)(codes + ((size_t)g * kb * 4 + (size_t)(k0 + min((uint32_t)d, n - 1)) * 4 + t) * 4096 +
+                                           j * 1024 + lane * 16);
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc += v[d][j].x ^ v[d][j].w;
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
 }
 
 // ---- read: one contiguous stream -------------------------------------------
@@ -440,8 +536,10 @@ static int run_read(size_t pool_mb) {
         CK(hipMemset(pool, 0x35, bytes * copies));
         const uint32_t subs = (sh.n + 31) / 32;
         static const char *const vname[] = {"tiles/2", "tiles/3", "linear", "sm/2", "g2w4/2", "g2w8/2", "g4w8/2",
-                                            "g4w16/2", "g2w4sm/2"};
-        for (int variant = 0; variant < 9; variant++) {
+                                            "g4w16/2", "g2w4sm/2", "t2+400nop", "t2+1600nop"};
+        const int nvar = getenv("Q35MM_PROBE_READ_PAD") ? 11 : 9;
+        for (int variant = 0; variant < nvar; variant++) {
+            if (nvar == 11 && variant > 0 && variant < 9) continue;
             if (variant >= 4 && subs % 4) continue;
             auto launch_on = [&](int i, hipStream_t s) {
                 const uint8_t *c = pool + (size_t)(i % copies) * bytes;
@@ -453,7 +551,9 @@ static int run_read(size_t pool_mb) {
                 else if (variant == 5) hipLaunchKernelGGL((read_group<2, 2, 8, false>), dim3(subs / 2), dim3(512), 0, s, c, kb, out);
                 else if (variant == 6) hipLaunchKernelGGL((read_group<2, 4, 8, false>), dim3(subs / 4), dim3(512), 0, s, c, kb, out);
                 else if (variant == 7) hipLaunchKernelGGL((read_group<2, 4, 16, false>), dim3(subs / 4), dim3(1024), 0, s, c, kb, out);
-                else hipLaunchKernelGGL((read_group<2, 2, 4, true>), dim3(subs / 2), dim3(256), 0, s, c, kb, out);
+                else if (variant == 8) hipLaunchKernelGGL((read_group<2, 2, 4, true>), dim3(subs / 2), dim3(256), 0, s, c, kb, out);
+                else if (variant == 9) hipLaunchKernelGGL(read_tiles_pad<400>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else hipLaunchKernelGGL(read_tiles_pad<1600>, dim3(subs), dim3(256), 0, s, c, kb, out);
             };
             auto launch = [&](int i) { launch_on(i, 0); };
             for (int i = 0; i < 8; i++) launch(i);
@@ -738,6 +838,154 @@ static int run_sync(bool spin) {
     return 0;
 }
 
+// Decode layer step of raw reads (qkv, o_proj, gate+up, down) over 8 layer
+// copies, 64 steps replayed as a graph.  PF = 0: reads only; PF = D > 0:
+// before each read, a prefetch_head<D> of the next launch's weight on a
+// second stream, depending (like the read) on the previous read only, so
+// the two run at the same time; REREAD: every weight read twice in a row
+// (the second read finds what the caches kept).
+static int run_step() {
+    struct Shape { uint32_t k, n; int depth; };
+    const Shape shapes[] = {{5120, 6144, 2}, {4096, 5120, 2}, {5120, 34816, 2}, {17408, 5120, 3}};
+    const int layers = 8, steps = 64;
+    std::vector<uint8_t *> w(layers * 4);
+    size_t step_bytes = 0;
+    for (int s = 0; s < 4; s++) step_bytes += (size_t)(shapes[s].n / 128) * (shapes[s].k / 128) * 16384;
+    for (int l = 0; l < layers; l++)
+        for (int s = 0; s < 4; s++) {
+            const size_t b = (size_t)(shapes[s].n / 128) * (shapes[s].k / 128) * 16384;
+            CK(hipMalloc(&w[l * 4 + s], b));
+            CK(hipMemset(w[l * 4 + s], 0x35, b));
+        }
+    float *out, *out2;
+    CK(hipMalloc(&out, 1 << 20));
+    CK(hipMalloc(&out2, 1 << 20));
+    hipStream_t a, b;
+    CK(hipStreamCreate(&a));
+    CK(hipStreamCreate(&b));
+    const int nev = steps * 4 + 1;
+    std::vector<hipEvent_t> ev(nev), evb(1);
+    for (auto &e : ev) CK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    CK(hipEventCreateWithFlags(&evb[0], hipEventDisableTiming));
+    hipEvent_t t0, t1;
+    CK(hipEventCreate(&t0));
+    CK(hipEventCreate(&t1));
+    auto read = [&](int i, hipStream_t st) {
+        const int s = i % 4, l = (i / 4) % layers;
+        const uint32_t kb = shapes[s].k / 128, subs = shapes[s].n / 32;
+        if (shapes[s].depth == 3)
+            hipLaunchKernelGGL(read_tiles<3>, dim3(subs), dim3(256), 0, st, w[l * 4 + s], kb, out);
+        else
+            hipLaunchKernelGGL(read_tiles<2>, dim3(subs), dim3(256), 0, st, w[l * 4 + s], kb, out);
+    };
+    auto prefetch = [&](int i, int D, uint32_t grid, hipStream_t st) {
+        const int s = i % 4, l = (i / 4) % layers;
+        const uint32_t kb = shapes[s].k / 128, subs = shapes[s].n / 32;
+        if (D == 1) hipLaunchKernelGGL(prefetch_head<1>, dim3(grid), dim3(256), 0, st, w[l * 4 + s], kb, subs, out2);
+        else if (D == 2) hipLaunchKernelGGL(prefetch_head<2>, dim3(grid), dim3(256), 0, st, w[l * 4 + s], kb, subs, out2);
+        else hipLaunchKernelGGL(prefetch_head<4>, dim3(grid), dim3(256), 0, st, w[l * 4 + s], kb, subs, out2);
+    };
+    struct Case { const char *name; int pf; uint32_t grid; bool reread; };
+    const Case cases[] = {{"reads only", 0, 0, false},          {"reads, each twice", 0, 0, true},
+                          {"prefetch 1 block, 64 wg", 1, 64, false}, {"prefetch 2 blocks, 64 wg", 2, 64, false},
+                          {"prefetch 2 blocks, 128 wg", 2, 128, false}, {"prefetch 4 blocks, 64 wg", 4, 64, false},
+                          {"reads only", 0, 0, false}};
+    for (const Case &c : cases) {
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        CK(hipStreamBeginCapture(a, hipStreamCaptureModeGlobal));
+        const int n = steps * 4;
+        for (int i = 0; i < n; i++) {
+            if (c.pf && i + 1 < n) {
+                // the prefetch of launch i+1 waits for launch i-1, as launch i does
+                if (i > 0) CK(hipStreamWaitEvent(b, ev[i - 1], 0));
+                else {
+                    CK(hipEventRecord(evb[0], a));
+                    CK(hipStreamWaitEvent(b, evb[0], 0));
+                }
+                prefetch(i + 1, c.pf, c.grid, b);
+            }
+            read(i, a);
+            if (c.reread) read(i, a);
+            CK(hipEventRecord(ev[i], a));
+        }
+        if (c.pf) {
+            CK(hipEventRecord(ev[n], b));
+            CK(hipStreamWaitEvent(a, ev[n], 0));
+        }
+        CK(hipStreamEndCapture(a, &g));
+        CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        CK(hipGraphLaunch(ge, a));
+        CK(hipStreamSynchronize(a));
+        double best = 1e30;
+        for (int r = 0; r < 3; r++) {
+            CK(hipEventRecord(t0, a));
+            CK(hipGraphLaunch(ge, a));
+            CK(hipEventRecord(t1, a));
+            CK(hipEventSynchronize(t1));
+            best = std::min(best, (double)time_ms(t0, t1) * 1e3 / steps);
+        }
+        printf("step of raw reads, %-26s %7.2f us per step  %6.0f GB/s\n", c.name, best,
+               step_bytes * (c.reread ? 2 : 1) / best / 1e3);
+        fflush(stdout);
+        CK(hipGraphExecDestroy(ge));
+        CK(hipGraphDestroy(g));
+    }
+    return 0;
+}
+
+// One decode layer step of raw reads with timestamps (after 16 warm-up
+// steps, launched back to back on one stream): per launch, the spread of
+// workgroup starts, time to the first block, end spread, gaps.
+static int run_stampread() {
+    struct Shape { const char *name; uint32_t k, n; int depth; };
+    const Shape shapes[] = {{"qkv", 5120, 6144, 2}, {"o_proj", 4096, 5120, 2}, {"gate+up", 5120, 34816, 2},
+                            {"down", 17408, 5120, 3}};
+    const int layers = 8;
+    std::vector<uint8_t *> w(layers * 4);
+    for (int l = 0; l < layers; l++)
+        for (int s = 0; s < 4; s++) {
+            const size_t b = (size_t)(shapes[s].n / 128) * (shapes[s].k / 128) * 16384;
+            CK(hipMalloc(&w[l * 4 + s], b));
+            CK(hipMemset(w[l * 4 + s], 0x35, b));
+        }
+    float *out;
+    CK(hipMalloc(&out, 1 << 20));
+    uint32_t *st[4];
+    for (int s = 0; s < 4; s++) CK(hipMalloc(&st[s], 3 * 1088 * sizeof(uint32_t)));
+    for (int it = 0; it < 17; it++)
+        for (int s = 0; s < 4; s++) {
+            const uint32_t kb = shapes[s].k / 128, subs = shapes[s].n / 32;
+            const uint8_t *c = w[(it % layers) * 4 + s];
+            if (shapes[s].depth == 3) hipLaunchKernelGGL(read_tiles_st<3>, dim3(subs), dim3(256), 0, 0, c, kb, out, st[s]);
+            else hipLaunchKernelGGL(read_tiles_st<2>, dim3(subs), dim3(256), 0, 0, c, kb, out, st[s]);
+        }
+    CK(hipDeviceSynchronize());
+    std::vector<std::vector<uint32_t>> h(4);
+    uint64_t base = ~0ull;
+    for (int s = 0; s < 4; s++) {
+        const uint32_t subs = shapes[s].n / 32;
+        h[s].resize(3 * subs);
+        CK(hipMemcpy(h[s].data(), st[s], 3 * subs * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        for (uint32_t i = 0; i < subs; i++) base = std::min<uint64_t>(base, h[s][3 * i]);
+    }
+    for (int s = 0; s < 4; s++) {
+        const uint32_t subs = shapes[s].n / 32;
+        std::vector<double> a(subs), f(subs), e(subs);
+        for (uint32_t i = 0; i < subs; i++) {
+            a[i] = (h[s][3 * i] - base) * 10.0;
+            f[i] = (h[s][3 * i + 1] - (double)h[s][3 * i]) * 10.0;
+            e[i] = (h[s][3 * i + 2] - base) * 10.0;
+        }
+        std::vector<double> fs = f;
+        std::sort(fs.begin(), fs.end());
+        printf("raw %-8s start %6.0f..%6.0f ns  first block med %5.0f max %5.0f  end %6.0f..%6.0f ns\n", shapes[s].name,
+               *std::min_element(a.begin(), a.end()), *std::max_element(a.begin(), a.end()), fs[subs / 2], fs.back(),
+               *std::min_element(e.begin(), e.end()), *std::max_element(e.begin(), e.end()));
+    }
+    return 0;
+}
+
 static int run_lds() {
     const uint32_t blocks = 256, iters = 4096;
     float *out;
@@ -771,7 +1019,9 @@ int main(int argc, char **argv) {
     if (argc >= 2 && !strcmp(argv[1], "mfma_rand")) return run_mfma_rand();
     if (argc >= 2 && !strcmp(argv[1], "mfma_order")) return run_mfma_order();
     if (argc >= 2 && !strcmp(argv[1], "launch")) return run_launch();
+    if (argc >= 2 && !strcmp(argv[1], "step")) return run_step();
+    if (argc >= 2 && !strcmp(argv[1], "stampread")) return run_stampread();
     if (argc >= 2 && !strcmp(argv[1], "sync")) return run_sync(argc >= 3 && !strcmp(argv[2], "spin"));
-    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma | mfma_rand | mfma_order | mix | launch | sync [spin]\n", argv[0]);
+    fprintf(stderr, "usage: %s read [pool_MB] | lds | mfma | mfma_rand | mfma_order | mix | launch | sync [spin] | step | stampread\n", argv[0]);
     return 2;
 }
