@@ -638,6 +638,7 @@ def main():
     mlp_out = None
     if args.mlp:
         H, I = base[GATE][1], base[GATE][2]
+        mlp_pair = os.environ.get("Q35MM_MLP_PAIR", "1")   # the library's default: paired gate and up
         gen = torch.Generator(device=dev).manual_seed(wl.SEED_BASE + 6)
         nws = [torch.randn(H, device=dev, generator=gen) * 0.1 for _ in range(args.pool)]
         xres = torch.randn((1, H), device=dev, generator=gen)
@@ -663,11 +664,18 @@ def main():
                    "GBps": round(blk_bytes * steps / el_b / 1e9, 1),
                    "frac_of_hbm_peak": round(blk_bytes * steps / el_b / 1e9 / HBM_PEAK_GBS, 4),
                    "us_matmuls_only": round(el_m / steps * 1e6, 2),
-                   "launches_per_block": 2 if rows_split_off else 4,
+                   "launches_per_block": 2 if rows_split_off or mlp_pair == "1" else 3 if mlp_pair == "2" else 4,
                    "note": ("q35mm_mlp at M=1: "
                             + ("RMSNorm (exact eight-lane order) inside the gate+up GEMV; SwiGLU and the residual "
                                "add inside the down GEMV"
                                if rows_split_off else
+                               "RMSNorm (exact eight-lane order, every workgroup) and SwiGLU inside one row-split "
+                               "launch over gate and up (16 rows of each per workgroup, one MFMA tile), the "
+                               "residual add inside the down GEMV"
+                               if mlp_pair == "1" else
+                               "RMSNorm as its own kernel, SwiGLU inside the paired gate+up launch, the residual "
+                               "add inside the down GEMV"
+                               if mlp_pair == "2" else
                                "RMSNorm and SwiGLU as their own kernels (gate, up and down run the row-split "
                                "GEMV, which takes plain activations), the residual add inside the down GEMV")
                             + "; us_matmuls_only = the gate+up and down GEMV launches on ready activations")}

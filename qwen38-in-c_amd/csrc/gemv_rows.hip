@@ -144,15 +144,22 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
 }  // namespace
 
 // MT = m rounded up to a power of two; DEPTH = ring depth; NW = wavefronts.
-template <bool VEC, uint32_t MT, uint32_t DEPTH, uint32_t NW>
+// MODE: kRowsPlain -- rows of up to four weights, y (+ resid) per segment;
+// kRowsPair -- the MLP's gate (segment 0) and up (segment 1) together,
+// writing silu(gate) * up; kRowsPairNorm -- the same on RMSNorm(x).
+template <bool VEC, uint32_t MT, uint32_t DEPTH, uint32_t NW, uint32_t MODE = kRowsPlain>
 __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
+    constexpr bool PAIR = MODE != kRowsPlain, NORM = MODE == kRowsPairNorm;
+    static_assert(!NORM || MT == 1, "the fused RMSNorm is for one token");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[NW][kGemvMaxM][kSubRows];
 
     uint32_t si = 0;
+    if constexpr (!PAIR) {
 #pragma unroll
-    for (uint32_t i = 1; i < 4; i++)
-        if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
+        for (uint32_t i = 1; i < 4; i++)
+            if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
+    }
     const GemvSeg &sg = p.seg[si];
     // Rows [r0, r1) of the segment: unit_rows rows per workgroup, or its Q
     // quads over its P workgroups, qbase = Q / P quads each and one more for
@@ -160,9 +167,15 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
     // No division here: every instruction a launch executes is fetched into
     // an instruction cache that starts cold at each launch (about 0.4 ns
     // per byte of code on this part), and a 64-bit division is ~800 bytes.
+    // Pair mode: workgroup c owns rows [16c, 16c + 16) of both weights;
+    // MFMA column n < 16 is gate row 16c + n, column 16 + n up row 16c + n,
+    // so silu(gate) * up is formed from the workgroup's own sums.
     const uint32_t c = blockIdx.x - sg.cta_begin;
     uint32_t r0, r1;
-    if (sg.unit_rows) {
+    if constexpr (PAIR) {
+        r0 = c * kPairRows;
+        r1 = min(r0 + kPairRows, sg.rows);
+    } else if (sg.unit_rows) {
         r0 = c * sg.unit_rows;
         r1 = min(r0 + sg.unit_rows, sg.rows);
     } else {
@@ -195,10 +208,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
     // blocks); v_readlane picks them per block, so no scalar load shares the
     // LDS counter with the operand reads inside the loop.  An output lane
     // (column mrow = row r0 + mrow) takes its row's group ----
-    const uint32_t ga = r0 >> 7, gb = (r1 - 1) >> 7;
+    // (Pair mode: a = gate's group, b = up's same group; lanes of columns
+    // 16..31 take up's.)
+    const uint32_t ga = r0 >> 7, gb = PAIR ? ga : (r1 - 1) >> 7;
+    const float *const scale_b = PAIR ? p.seg[1].scale : sg.scale;
     const float sca_lane = sg.scale[(size_t)ga * KB + kbof(min(lane, n - 1))];
-    const float scb_lane = sg.scale[(size_t)gb * KB + kbof(min(lane, n - 1))];
-    const bool out_in_a = ((r0 + mrow) >> 7) == ga;
+    const float scb_lane = scale_b[(size_t)gb * KB + kbof(min(lane, n - 1))];
+    const bool out_in_a = PAIR ? mrow < kPairRows : ((r0 + mrow) >> 7) == ga;
 
     // ---- ring: slot d holds the weights of block b and the activations of
     // block b+1 (clamped into the range).  Weights are read once per call:
@@ -206,24 +222,68 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
     // +3.4% against plain loads) ----
     // lane l: row r0 + l%32 (clamped into the range; the extra columns are
     // never written), its sub-tile and place in the 1 KiB chunks
-    const uint32_t rl = min(r0 + mrow, r1 - 1);
-    const uint8_t *codes = sg.codes + ((size_t)(rl >> 7) * KB * 4 + ((rl >> 5) & 3)) * kSubBytes + hh * 512 +
+    const uint32_t rl = min(r0 + (PAIR ? mrow % kPairRows : mrow), r1 - 1);
+    const uint8_t *const codes_w = PAIR && mrow >= kPairRows ? p.seg[1].codes : sg.codes;
+    const uint8_t *codes = codes_w + ((size_t)(rl >> 7) * KB * 4 + ((rl >> 5) & 3)) * kSubBytes + hh * 512 +
                            (rl & 31) * 16;
     u32x4_t buf[DEPTH][4];
-    XBlock<MT> xr[DEPTH];
+    XBlock<MT> xr[DEPTH], wr[NORM ? DEPTH : 1];   // wr: RMSNorm weights of the same columns
     auto load = [&](uint32_t d, uint32_t i) {
         const uint8_t *src = codes + (size_t)kbof(i) * kBlockBytes;
 #pragma unroll
         for (uint32_t j = 0; j < 4; j++)
             buf[d][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(src + j * kChunkBytes));
         load_xblock<VEC, MT>(xr[d], p.x, p.ldx, M, p.k, kbof(min(i + 1, n - 1)), lane);
+        if constexpr (NORM) load_xblock<VEC, MT>(wr[d], p.norm_w, 0, 1, p.k, kbof(min(i + 1, n - 1)), lane);
     };
-    XBlock<MT> x0;
+    // RMSNorm: the row's whole x, squared into LDS for the reference's
+    // eight sequential lane sums (loaded first, so waiting for it waits for
+    // nothing else)
+    constexpr uint32_t kNormPer = NORM ? kPairNormMaxCols / (64 * NW) : 1;
+    float xs[kNormPer];
+    if constexpr (NORM) {
+#pragma unroll
+        for (uint32_t j = 0; j < kNormPer; j++) {
+            const uint32_t i = threadIdx.x + j * 64 * NW;
+            xs[j] = i < p.k ? p.x[i] : 0.0f;
+        }
+    }
+    XBlock<MT> x0, w0;
     load_xblock<VEC, MT>(x0, p.x, p.ldx, M, p.k, kbof(0), lane);
+    if constexpr (NORM) load_xblock<VEC, MT>(w0, p.norm_w, 0, 1, p.k, kbof(0), lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (uint32_t d = 0; d + 1 < DEPTH; d++) load(d, min(d, n - 1));
     __builtin_amdgcn_sched_barrier(0);
+    // The scale 1 / sqrt(mean(x^2) + eps) of the row, computed by every
+    // workgroup while its first weight loads are in flight (the
+    // workgroups of a launch are resident together, so this costs the
+    // launch one chain of n/8 dependent adds, not one per workgroup)
+    float inv = 1.0f;
+    if constexpr (NORM) {
+        __shared__ float s_inv;
+        float *const sq = reinterpret_cast<float *>(lds + NW * gemv_rows_wave_lds(1));
+        const uint32_t kStride = pair_norm_stride(p.k);
+        const uint32_t kpad = (p.k + 7) & ~7u;   // squares the lane sums read; past the row +0, no change
+#pragma unroll
+        for (uint32_t j = 0; j < kNormPer; j++) {
+            const uint32_t i = threadIdx.x + j * 64 * NW;
+            if (i < kpad) sq[(i & 7) * kStride + (i >> 3)] = xs[j] * xs[j];
+        }
+        __syncthreads();
+        if (threadIdx.x < 8) red[0][0][threadIdx.x] = lane_sum_in_order(sq + threadIdx.x * kStride, (p.k + 7) >> 3, 0.0f);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = red[0][0][0];
+#pragma unroll
+            for (uint32_t j = 1; j < 8; j++) sum = sum + red[0][0][j];
+            s_inv = rms_inverse(sum, p.k, p.eps);
+        }
+        __syncthreads();
+        inv = s_inv;
+#pragma unroll
+        for (uint32_t e = 0; e < XBlock<MT>::kG; e++) x0.v[e] = rmsnorm1(x0.v[e], inv, w0.v[e]);
+    }
     stage_xblock<MT>(x0, wbase, M, R, p.k, kbof(0), lane);   // waits for x0 only: loads complete in order
 
     // ---- stream ----
@@ -242,6 +302,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
 #pragma unroll
                 for (uint32_t i = 0; i < 8; i++)
                     araw[i] = *reinterpret_cast<const u32x4_t *>(arow + par * a_slot + i * a_step);
+                if constexpr (NORM) {
+#pragma unroll
+                    for (uint32_t e = 0; e < XBlock<MT>::kG; e++) xr[d].v[e] = rmsnorm1(xr[d].v[e], inv, wr[d].v[e]);
+                }
                 if (bb + 1 < n) stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, kbof(bb + 1), lane);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16_t part;
@@ -276,6 +340,22 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
         if (t < M) red[wv][t][mrow] = (acc[r] + acc[r + 4]) + acc[r + 8];
     }
     __syncthreads();
+    if constexpr (PAIR) {
+        // gate and up of row r0 + n, wavefronts added in order as for one
+        // weight, then silu(gate) * up (the bits of the separate kernels)
+        if (threadIdx.x < kPairRows * M) {
+            const uint32_t t = threadIdx.x / kPairRows, n = threadIdx.x % kPairRows;
+            float g = red[0][t][n], u = red[0][t][n + kPairRows];
+#pragma unroll
+            for (uint32_t w = 1; w < NW; w++) {
+                g += red[w][t][n];
+                u += red[w][t][n + kPairRows];
+            }
+            const uint32_t row = r0 + n;
+            if (row < r1) sg.y[(size_t)t * sg.ldy + row] = swiglu1(g, u);
+        }
+        return;
+    }
     if (threadIdx.x < kSubRows * M) {
         const uint32_t t = threadIdx.x >> 5, n = threadIdx.x & 31;
         float sum = red[0][t][n];
@@ -325,7 +405,51 @@ RowsKernel rows_kernel(uint32_t depth, uint32_t vec_mt) {
 #undef Q35_RK
     return k[depth - 2][vec_mt];
 }
+using PairKernel = void (*)(GemvParams);
+PairKernel pair_kernel(bool norm, uint32_t depth, uint32_t vec_mt) {
+#define Q35_PK(D)                                                                                       \
+    {gemv_rows_kernel<false, 1, D, 4, kRowsPair>, gemv_rows_kernel<false, 2, D, 4, kRowsPair>,          \
+     gemv_rows_kernel<false, 4, D, 4, kRowsPair>, gemv_rows_kernel<false, 8, D, 4, kRowsPair>,          \
+     gemv_rows_kernel<true, 1, D, 4, kRowsPair>,  gemv_rows_kernel<true, 2, D, 4, kRowsPair>,           \
+     gemv_rows_kernel<true, 4, D, 4, kRowsPair>,  gemv_rows_kernel<true, 8, D, 4, kRowsPair>}
+    static const PairKernel k[2][8] = {Q35_PK(2), Q35_PK(3)};
+#undef Q35_PK
+    static const PairKernel kn[2][2] = {{gemv_rows_kernel<false, 1, 2, 4, kRowsPairNorm>,
+                                         gemv_rows_kernel<true, 1, 2, 4, kRowsPairNorm>},
+                                        {gemv_rows_kernel<false, 1, 3, 4, kRowsPairNorm>,
+                                         gemv_rows_kernel<true, 1, 3, 4, kRowsPairNorm>}};
+    return norm ? kn[depth - 2][vec_mt >> 2] : k[depth - 2][vec_mt];
+}
 }  // namespace
+
+hipError_t launch_gemv_pair(const GemvParams &pin, bool norm, uint32_t cus, hipStream_t stream) {
+    GemvParams p = pin;
+    const GemvSeg &g = p.seg[0], &u = p.seg[1];
+    if (p.xmode != kXPlain || p.m == 0 || p.m > kGemvMaxM || !gemv_rows_shape(p.kb, 4) || p.nseg != 2 ||
+        g.rows != u.rows || g.nb != u.nb || g.rows == 0 || g.cta_begin != 0)
+        return hipErrorInvalidValue;
+    if (norm && (p.m != 1 || p.k > kPairNormMaxCols || !p.norm_w)) return hipErrorInvalidValue;
+    p.nctas = (g.rows + kPairRows - 1) / kPairRows;
+    size_t lds = 4 * (size_t)gemv_rows_wave_lds(p.m);
+    if (norm) lds += 8 * pair_norm_stride(p.k) * sizeof(float);   // the squares of x, lane-major
+    const uint32_t mt = p.m <= 1 ? 0 : p.m <= 2 ? 1 : p.m <= 4 ? 2 : 3;
+    const uint32_t depth = p.m <= 2 && p.nctas <= cus ? kRsDepthLong : kRsDepthShort;
+    const PairKernel k = pair_kernel(norm, depth, (p.x_vec ? 4 : 0) + mt);
+    static bool attr_set = false;
+    if (!attr_set) {
+        for (bool nm : {false, true})
+            for (uint32_t d : {2u, 3u})
+                for (uint32_t v = 0; v < 8; v++) {
+                    if (nm && (v & 3)) continue;
+                    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(pair_kernel(nm, d, v)),
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+                    if (e != hipSuccess) return e;
+                }
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(k, dim3(p.nctas), dim3(256), lds, stream, p);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv_rows(const GemvParams &pin, uint32_t cus, uint32_t waves, uint32_t depth,
                             hipStream_t stream) {

@@ -137,6 +137,19 @@ void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t cus, uint32_t 
 // waves: 4 or 8; depth: ring depth 2..4 (0: by launch shape).
 hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, uint32_t waves, uint32_t depth, hipStream_t stream);
 
+// Row-split kernel modes: plain rows of up to four weights, or the MLP's
+// gate (seg[0]) and up (seg[1]) paired -- kPairRows rows of each per
+// workgroup, one MFMA tile -- writing silu(gate) * up to seg[0].y, on x as
+// given (kRowsPair) or on RMSNorm(x) with p.norm_w / p.eps (kRowsPairNorm,
+// one token, k <= kPairNormMaxCols: every workgroup forms the row's scale).
+constexpr uint32_t kRowsPlain = 0, kRowsPair = 1, kRowsPairNorm = 2;
+constexpr uint32_t kPairRows = 16;
+constexpr uint32_t kPairNormMaxCols = 8192;
+// Floats per lane row of the fused RMSNorm's squares in LDS ([8][stride]):
+// k/8 rounded up to whole float4, + 4 to spread the eight rows over banks.
+__host__ __device__ constexpr uint32_t pair_norm_stride(uint32_t k) { return (((k + 7) / 8 + 3) & ~3u) + 4; }
+hipError_t launch_gemv_pair(const GemvParams &p, bool norm, uint32_t cus, hipStream_t stream);
+
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
 constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64

@@ -110,6 +110,8 @@ struct Device {
     bool trust_pointers = false;
     bool verify_full = false;   // Q35MM_VERIFY_WEIGHTS=full: fingerprint every byte of a reused host weight
     bool mlp_unfused = false;   // Q35MM_MLP_UNFUSED=1: separate neighbour kernels on the GEMV path
+    uint32_t mlp_pair = 1;      // Q35MM_MLP_PAIR=0: row-split gate and up as plain GEMV launches;
+                                //   2: paired, with the RMSNorm as its own kernel
     bool gemv_rows = true;      // Q35MM_GEMV_ROWSPLIT=0: every weight on the stream-K GEMV
     uint32_t rows_depth = 0;    // Q35MM_ROWS_DEPTH: ring depth of the row-split GEMV (0: by launch)
     uint32_t rows_waves = 4;    // Q35MM_ROWS_WAVES: wavefronts per row-split workgroup (4 or 8)
@@ -141,6 +143,7 @@ int ensure_device() {
         g_dev.verify_full = v && strcmp(v, "full") == 0;
     }
     g_dev.mlp_unfused = env_u32("Q35MM_MLP_UNFUSED", 0) != 0;
+    g_dev.mlp_pair = env_u32("Q35MM_MLP_PAIR", 1);
     {
         const char *v = getenv("Q35MM_HOST_WAIT");
         g_dev.done_spin = !(v && strcmp(v, "sync") == 0);
@@ -1279,6 +1282,38 @@ Q35MM_API int q35mm_swiglu(const float *dGate, const float *dUp, float *dY, size
     return Q35MM_OK;
 }
 
+// silu(x @ gate^T) * (x @ up^T) for m <= kGemvMaxM tokens of row-split gate
+// and up weights in one launch (gemv_rows_kernel, pair mode), on RMSNorm(x)
+// when norm_w is given (one token): the bits of rmsnorm, the gate+up GEMV
+// and swiglu as separate kernels.
+int run_mlp_pair(const q35mm_weight *gate, const q35mm_weight *up, uint32_t m, const float *dX, const float *norm_w,
+                 float eps, float *dH, hipStream_t st) {
+    const Weight &g = gate->w, &u = up->w;
+    GemvParams p{};
+    p.x = dX;
+    p.norm_w = norm_w;
+    p.eps = eps;
+    p.xmode = kXPlain;
+    p.ldx = g.cols;
+    p.m = m;
+    p.k = g.cols;
+    p.kb = g.kb;
+    p.nseg = 2;
+    p.x_vec = (aligned16(dX) && g.cols % 8 == 0 && (!norm_w || aligned16(norm_w))) ? 1u : 0u;
+    const Weight *ws[2] = {&g, &u};
+    for (uint32_t s = 0; s < 2; s++) {
+        GemvSeg &sg = p.seg[s];
+        sg.codes = ws[s]->codes;
+        sg.scale = ws[s]->scale;
+        sg.y = dH;
+        sg.rows = ws[s]->rows;
+        sg.ldy = ws[s]->rows;
+        sg.nb = ws[s]->nb;
+    }
+    HIP_TRY(launch_gemv_pair(p, norm_w != nullptr, g_dev.cus, st));
+    return Q35MM_OK;
+}
+
 Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const q35mm_weight *down,
                         const float *dNormW, float eps, uint32_t m, float *dX, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
@@ -1312,6 +1347,23 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         // A row-split weight takes plain activations: its neighbour runs as
         // the separate kernel, which gives the same bits.
         const uint32_t mg = std::min(m, kGemvMaxM);
+        const q35mm_weight *dn[1] = {down};
+        float *dy[1] = {dX};
+        if (!g_dev.mlp_unfused && g_dev.mlp_pair && uses_gemv_rows(gate->w) && uses_gemv_rows(up->w)) {
+            // Row-split gate and up (the model's shapes): one launch per
+            // group of up to eight tokens forms silu(gate) * up, with the
+            // RMSNorm inside for one token; then the down GEMV with the
+            // residual add.
+            const bool norm_in = m == 1 && H <= kPairNormMaxCols && g_dev.mlp_pair == 1;
+            if (!norm_in) HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
+            for (uint32_t t0 = 0; t0 < m; t0 += kGemvMaxM) {
+                const uint32_t mt = std::min(kGemvMaxM, m - t0);
+                rc = run_mlp_pair(gate, up, mt, (norm_in ? dX : xn) + (size_t)t0 * H, norm_in ? dNormW : nullptr, eps,
+                                  g + (size_t)t0 * I, st);
+                if (rc) return rc;
+            }
+            return run_gemv(dn, 1, m, g, dy, st, GemvInput(), dy);
+        }
         const bool fuse_norm = !g_dev.mlp_unfused && gemv_norm_fits(mg, H) && !uses_gemv_rows(gate->w) &&
                                !uses_gemv_rows(up->w);
         const bool fuse_swiglu = !g_dev.mlp_unfused && m <= kMlpFusedSwiGLUMaxM && !uses_gemv_rows(down->w);
@@ -1335,8 +1387,6 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         } else {
             HIP_TRY(launch_swiglu(g, u, g, ni, st));
         }
-        const q35mm_weight *dn[1] = {down};
-        float *dy[1] = {dX};
         if (!g_dev.mlp_unfused) return run_gemv(dn, 1, m, g, dy, st, sw, dy);
         rc = run_gemv(dn, 1, m, g, &y, st, sw);
         if (rc) return rc;

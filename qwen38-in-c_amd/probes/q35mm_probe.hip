@@ -160,6 +160,38 @@ __global__ __launch_bounds__(256) void read_tiles_st(const uint8_t *codes, uint3
     }
 }
 
+// read_tiles<3> whose unrolled loop carries NOPS s_nop per block copy
+// (executed every block, in the shadow of the memory wait): what a larger
+// loop body costs once per launch when its code is fetched cold.
+template <int NOPS>
+__global__ __launch_bounds__(256) void read_tiles_fat(const uint8_t *codes, uint32_t kb, float *out) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t sub = blockIdx.x, g = sub >> 2, s = sub & 3;
+    const uint32_t k0 = wv * kb / 4, n = (wv + 1) * kb / 4 - k0;
+    const uint8_t *b = codes + ((size_t)g * kb * 4 + s) * 4096 + (size_t)k0 * 16384 + lane * 16;
+    constexpr int D = 3;
+    u32x4 buf[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int d = 0; d < D; d++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min((uint32_t)d, n - 1) * 16384 + j * 1024));
+    for (uint32_t i = 0; i < n; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (i + d < n) acc += buf[d][j].x ^ buf[d][j].w;
+                buf[d][j] = __builtin_nontemporal_load((const u32x4 *)(b + (size_t)min(i + d + D, n - 1) * 16384 + j * 1024));
+            }
+            if constexpr (NOPS == 64) asm volatile(".rept 64\n s_nop 0\n .endr");
+            if constexpr (NOPS == 256) asm volatile(".rept 256\n s_nop 0\n .endr");
+        }
+    }
+    if (lane == 0) out[blockIdx.x * 4 + wv] = (float)acc;
+}
+
 // ---- read: S sub-tiles per workgroup, W wavefronts splitting K -------------------
 // S = 2: 64 rows per workgroup, S = 4: a whole 128-row group (16 KiB per K
 // block).  SM: the weight as if stored sub-tile-major (each 32-row
@@ -536,10 +568,11 @@ static int run_read(size_t pool_mb) {
         CK(hipMemset(pool, 0x35, bytes * copies));
         const uint32_t subs = (sh.n + 31) / 32;
         static const char *const vname[] = {"tiles/2", "tiles/3", "linear", "sm/2", "g2w4/2", "g2w8/2", "g4w8/2",
-                                            "g4w16/2", "g2w4sm/2", "t2+400nop", "t2+1600nop"};
-        const int nvar = getenv("Q35MM_PROBE_READ_PAD") ? 11 : 9;
+                                            "g4w16/2", "g2w4sm/2", "t2+400nop", "t2+1600nop", "t3+64nop/blk",
+                                            "t3+256nop/blk"};
+        const int nvar = getenv("Q35MM_PROBE_READ_PAD") ? 13 : 9;
         for (int variant = 0; variant < nvar; variant++) {
-            if (nvar == 11 && variant > 0 && variant < 9) continue;
+            if (nvar == 13 && variant > 1 && variant < 9) continue;
             if (variant >= 4 && subs % 4) continue;
             auto launch_on = [&](int i, hipStream_t s) {
                 const uint8_t *c = pool + (size_t)(i % copies) * bytes;
@@ -553,7 +586,9 @@ static int run_read(size_t pool_mb) {
                 else if (variant == 7) hipLaunchKernelGGL((read_group<2, 4, 16, false>), dim3(subs / 4), dim3(1024), 0, s, c, kb, out);
                 else if (variant == 8) hipLaunchKernelGGL((read_group<2, 2, 4, true>), dim3(subs / 2), dim3(256), 0, s, c, kb, out);
                 else if (variant == 9) hipLaunchKernelGGL(read_tiles_pad<400>, dim3(subs), dim3(256), 0, s, c, kb, out);
-                else hipLaunchKernelGGL(read_tiles_pad<1600>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else if (variant == 10) hipLaunchKernelGGL(read_tiles_pad<1600>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else if (variant == 11) hipLaunchKernelGGL(read_tiles_fat<64>, dim3(subs), dim3(256), 0, s, c, kb, out);
+                else hipLaunchKernelGGL(read_tiles_fat<256>, dim3(subs), dim3(256), 0, s, c, kb, out);
             };
             auto launch = [&](int i) { launch_on(i, 0); };
             for (int i = 0; i < 8; i++) launch(i);

@@ -194,14 +194,18 @@ def test_mlp_block_real_shape(q, oracle, wl, gpu, m):
 
 
 @pytest.mark.parametrize("m,H,I", [(1, 640, 1664), (2, 640, 1664), (8, 5120, 1024), (13, 645, 1000),
-                                   (1, 8200, 256), (1, 5120, 17408), (64, 640, 1664), (100, 645, 1000)])
+                                   (1, 8200, 256), (1, 5120, 17408), (64, 640, 1664), (100, 645, 1000),
+                                   (1, 645, 1000), (1, 520, 1000), (1, 8192, 272)])
 def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
     """The block entry point gives the bits of the separate device calls it
     stands for (rmsnorm, gate+up, swiglu, down, add), whichever fusion the
-    shapes select.  Decode path: RMSNorm in the gate+up GEMV; SwiGLU in a
-    stream-K down GEMV's staging (m <= 2) or as its own kernel (row-split
-    down, as in the model's 5120 x 17408 block here, or m > 2); the residual
-    add in the down GEMV.  Prefill path (m >= 64): gate and up as one GEMM
+    shapes select.  Decode path with row-split gate and up (K of 4..160
+    blocks, the model's shapes): one launch pairs 16 rows of gate with the
+    same 16 of up per workgroup and writes silu(gate) * up, with the RMSNorm
+    inside for one token of up to 8192 columns (ragged H and I here, and
+    rows beyond a multiple of 16); otherwise RMSNorm in a stream-K gate+up
+    GEMV, SwiGLU in a stream-K down GEMV's staging (m <= 2) or as its own
+    kernel; the residual add in the down GEMV.  Prefill path (m >= 64): gate and up as one GEMM
     launch, SwiGLU while the down GEMM rounds its activations to bf16, the
     residual add in the down GEMM's epilogue."""
     import torch
