@@ -37,7 +37,9 @@ def _host(t):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1003, 4100), (4, 1003, 4100), (5, 1000, 4065), (8, 8192, 8192),
                                    (3, 4096, 5120), (8, 5120, 6144), (2, 1024, 7777), (6, 20480, 4100),
-                                   (7, 17400, 5000), (1, 1024, 20000), (3, 2048, 9001)])
+                                   (7, 17400, 5000), (1, 1024, 20000), (3, 2048, 9001),
+                                   # aligned rows, a last block of 8 columns (k % 16 == 8)
+                                   (8, 1032, 4100), (4, 1032, 4100)])
 def test_row_split_shapes(q, oracle, wl, gpu, m, k, n):
     W, sc = wl.gen_weight_ragged(7 * n + k + m, n, k)
     X = wl.gen_act(n + m, m, k, outlier_frac=0.01)
