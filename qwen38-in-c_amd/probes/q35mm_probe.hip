@@ -831,6 +831,22 @@ __global__ __launch_bounds__(64) void flag_kernel(volatile uint32_t *flag, uint3
     }
 }
 
+// The empty kernel whose last workgroup to finish stores the flag: each
+// workgroup's thread 0 makes its stores visible system-wide, then counts
+// itself in; the last one resets the counter and stores v.
+__global__ __launch_bounds__(256) void empty_flag_kernel(float *out, uint32_t *count, uint32_t *flag, uint32_t v) {
+    if (threadIdx.x == 0) {
+        if (out) out[blockIdx.x] = 0.0f;
+        __threadfence_system();
+        const uint32_t prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == gridDim.x - 1) {
+            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __threadfence_system();
+            __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
 static int run_sync(bool spin) {
     if (spin) CK(hipSetDeviceFlags(hipDeviceScheduleSpin));
     hipStream_t st;
@@ -843,15 +859,41 @@ static int run_sync(bool spin) {
     hipEvent_t ev;
     CK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     const int n = 2000;
-    for (int mode = 0; mode < 3; mode++) {
+    // spins give up after a second: a missing store ends the probe, not the box
+    auto spin_for = [&](uint32_t v) {
+        const auto ts = std::chrono::steady_clock::now();
+        for (uint32_t j = 0; __atomic_load_n(flag, __ATOMIC_ACQUIRE) != v; j++) {
+            __builtin_ia32_pause();
+            if ((j & 1023) == 1023 && std::chrono::steady_clock::now() - ts > std::chrono::seconds(1)) {
+                fprintf(stderr, "flag %u never came\n", v);
+                exit(1);
+            }
+        }
+    };
+    uint32_t *count;
+    CK(hipMalloc(&count, 64));
+    CK(hipMemset(count, 0, 64));
+    CK(hipDeviceSynchronize());
+    for (int mode = 0; mode < 6; mode++) {
         double best = 1e30;
         for (int rep = 0; rep < 3; rep++) {
             auto t0 = std::chrono::steady_clock::now();
             for (int i = 0; i < n; i++) {
+                const uint32_t v = (uint32_t)(mode * 3 * n + rep * n + i + 1);
                 if (mode == 2) {
-                    const uint32_t v = (uint32_t)(rep * n + i + 1);
                     hipLaunchKernelGGL(flag_kernel, dim3(1), dim3(64), 0, st, (volatile uint32_t *)flag, v);
-                    while (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != v) __builtin_ia32_pause();
+                    spin_for(v);
+                } else if (mode == 3) {
+                    hipLaunchKernelGGL(empty_kernel, dim3(160), dim3(256), 0, st, out);
+                    hipLaunchKernelGGL(flag_kernel, dim3(1), dim3(64), 0, st, (volatile uint32_t *)flag, v);
+                    spin_for(v);
+                } else if (mode == 5) {
+                    hipLaunchKernelGGL(empty_flag_kernel, dim3(160), dim3(256), 0, st, out, count, flag, v);
+                    spin_for(v);
+                } else if (mode == 4) {
+                    hipLaunchKernelGGL(empty_kernel, dim3(160), dim3(256), 0, st, out);
+                    CK(hipStreamWriteValue32(st, flag, v, 0));
+                    spin_for(v);
                 } else {
                     hipLaunchKernelGGL(empty_kernel, dim3(160), dim3(256), 0, st, out);
                     if (mode == 0) {
@@ -866,8 +908,14 @@ static int run_sync(bool spin) {
             const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() / n;
             best = std::min(best, us);
         }
-        printf("host round trip (%s scheduling), launch + %s: %.2f us\n", spin ? "spin" : "default",
-               mode == 0 ? "hipStreamSynchronize" : mode == 1 ? "hipEventSynchronize" : "spin on a pinned flag", best);
+        printf("host round trip (%s scheduling), %s: %.2f us\n", spin ? "spin" : "default",
+               mode == 0   ? "launch + hipStreamSynchronize"
+               : mode == 1 ? "launch + hipEventSynchronize"
+               : mode == 2 ? "flag-kernel launch + spin on the pinned flag"
+               : mode == 3 ? "launch + flag-kernel launch + spin"
+               : mode == 4 ? "launch + hipStreamWriteValue32 of the flag + spin"
+                           : "launch of a kernel whose last workgroup stores the flag + spin",
+               best);
         fflush(stdout);
     }
     return 0;
