@@ -17,15 +17,16 @@
 // protocol costs a few microseconds per launch, as much as streaming these
 // weights takes.
 //
-// Ranges (gemv_rows_plan).  A launch whose weights hold at least half as
-// many 32-row sub-tiles as the device has CUs runs one workgroup per
-// sub-tile: each load is a whole 1 KiB chunk, which the memory system
-// streams fastest (a raw-read probe of 5120 x 17408 codes: 15.2 us as
+// Ranges (gemv_rows_plan).  One workgroup per 32-row sub-tile, whatever
+// the launch's size: each load is a whole 1 KiB chunk, which the memory
+// system streams fastest (a raw-read probe of 5120 x 17408 codes: 15.2 us as
 // sub-tiles on 160 CUs against 17.5 us as 256 ranges of 20 rows, whose
-// loads read 320-byte pieces of each chunk).  Smaller launches (the
-// model's 1024-row k/v projections, 48-row DeltaNet gates) would leave most
-// CUs idle that way; they get one workgroup per CU, each a balanced range
-// of whole 4-row quads (which may straddle sub-tiles and scale groups).
+// loads read 320-byte pieces of each chunk).  A small launch leaves most
+// CUs idle that way and is still no slower than spreading its rows over
+// every CU in ranges of 4 rows: 1024 x 5120 6.05 against 6.48 us, 256 x
+// 17408 14.0 against 14.3 us; such a launch is bound by each wavefront's
+// chain of K blocks (about 0.35 us of instructions per block at one
+// wavefront per SIMD), not by how many CUs stream.
 
 // Arithmetic is the stream-K kernel's: e4m3 -> bf16 exactly, activations
 // split exactly into three bf16 parts (A-operand rows m = token + 8*part),
@@ -172,27 +173,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
             if (i < p.nseg && blockIdx.x >= p.seg[i].cta_begin) si = i;
     }
     const GemvSeg &sg = p.seg[si];
-    // Rows [r0, r1) of the segment: unit_rows rows per workgroup, or its Q
-    // quads over its P workgroups, qbase = Q / P quads each and one more for
-    // the first qrem = Q % P (the host keeps P <= Q and ceil(Q/P) <= 8).
-    // No division here: every instruction a launch executes is fetched into
-    // an instruction cache that starts cold at each launch (about 0.4 ns
-    // per byte of code on this part), and a 64-bit division is ~800 bytes.
-    // Pair mode: workgroup c owns rows [16c, 16c + 16) of both weights;
-    // MFMA column n < 16 is gate row 16c + n, column 16 + n up row 16c + n,
-    // so silu(gate) * up is formed from the workgroup's own sums.
+    // Rows [r0, r1) of the segment: workgroup c owns sub-tile c.  Pair
+    // mode: workgroup c owns rows [16c, 16c + 16) of both weights; MFMA
+    // column n < 16 is gate row 16c + n, column 16 + n up row 16c + n, so
+    // silu(gate) * up is formed from the workgroup's own sums.
     const uint32_t c = blockIdx.x - sg.cta_begin;
-    uint32_t r0, r1;
-    if constexpr (PAIR) {
-        r0 = c * kPairRows;
-        r1 = min(r0 + kPairRows, sg.rows);
-    } else if (sg.unit_rows) {
-        r0 = c * sg.unit_rows;
-        r1 = min(r0 + sg.unit_rows, sg.rows);
-    } else {
-        r0 = 4 * (c * sg.qbase + min(c, sg.qrem));
-        r1 = min(4 * ((c + 1) * sg.qbase + min(c + 1, sg.qrem)), sg.rows);
-    }
+    const uint32_t unit = PAIR ? kPairRows : kSubRows;
+    const uint32_t r0 = c * unit, r1 = min(r0 + unit, sg.rows);
     const uint32_t KB = p.kb, M = p.m, R = stage_rows(M);
 
     const uint32_t lane = threadIdx.x & 63;
@@ -382,25 +369,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
 
 bool gemv_rows_shape(uint32_t kb, uint32_t waves) { return kb >= waves && kb <= kGemvRsMaxKb && kb <= 64 * waves; }
 
-void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t cus, uint32_t *nctas, uint32_t *unit_rows) {
-    uint64_t tot = 0, subs = 0;
-    for (uint32_t s = 0; s < nseg; s++) {
-        tot += rows[s];
-        subs += (rows[s] + kSubRows - 1) / kSubRows;
-    }
-    for (uint32_t s = 0; s < nseg; s++) {
-        if (2 * subs >= cus) {
-            nctas[s] = (rows[s] + kSubRows - 1) / kSubRows;
-            unit_rows[s] = kSubRows;
-            continue;
-        }
-        const uint64_t q = (rows[s] + 3) / 4;
-        uint64_t ps = tot ? (uint64_t)cus * rows[s] / tot : 1;
-        ps = std::max<uint64_t>(ps, (q + 7) / 8);   // at most 8 quads = 32 rows each
-        ps = std::min<uint64_t>(ps, q);             // every range holds a quad
-        nctas[s] = (uint32_t)std::max<uint64_t>(ps, 1);
-        unit_rows[s] = 0;
-    }
+void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t *nctas) {
+    for (uint32_t s = 0; s < nseg; s++) nctas[s] = (rows[s] + kSubRows - 1) / kSubRows;
 }
 
 namespace {
@@ -469,17 +439,9 @@ hipError_t launch_gemv_rows(const GemvParams &pin, uint32_t cus, uint32_t waves,
         !gemv_rows_shape(p.kb, waves) || p.nseg == 0 || p.nseg > 4)
         return hipErrorInvalidValue;
     for (uint32_t s = 0; s < p.nseg; s++) {
-        GemvSeg &g = p.seg[s];
-        if (!g.unit_rows && g.nctas) {
-            const uint32_t q = (g.rows + 3) / 4;
-            g.qbase = q / g.nctas;
-            g.qrem = q % g.nctas;
-        }
-        const uint32_t q = (g.rows + 3) / 4;
-        const bool ok = g.unit_rows ? g.unit_rows <= kSubRows && (uint64_t)g.nctas * g.unit_rows >= g.rows &&
-                                          (uint64_t)(g.nctas - 1) * g.unit_rows < g.rows
-                                    : g.nctas > 0 && g.nctas <= q && (q + g.nctas - 1) / g.nctas <= 8;
-        if (!ok) return hipErrorInvalidValue;   // every range must hold 1..32 rows
+        const GemvSeg &g = p.seg[s];
+        if (g.rows == 0 || g.nctas != (g.rows + kSubRows - 1) / kSubRows)
+            return hipErrorInvalidValue;   // one workgroup per 32-row sub-tile
     }
     const size_t lds = (size_t)waves * gemv_rows_wave_lds(p.m);
     const uint32_t mt = p.m <= 1 ? 0 : p.m <= 2 ? 1 : p.m <= 4 ? 2 : 3;   // log2 of MT

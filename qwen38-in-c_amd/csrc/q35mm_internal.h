@@ -58,9 +58,6 @@ struct GemvSeg {
     uint32_t maxc;       // contributions per group the workspace holds
     uint32_t ws_off;     // float offset of the segment's partials [nb][maxc][8][128]
     uint32_t cnt_off;    // offset of the segment's arrival counters [nb]
-    uint32_t unit_rows;  // row-split GEMV: rows per workgroup (0: balanced 4-row quads)
-    uint32_t qbase;      // row-split quads: every range holds qbase quads,
-    uint32_t qrem;       //   the first qrem ranges one more (set by launch_gemv_rows)
 };
 
 // What the staged activations are, per column k of token t:
@@ -115,8 +112,8 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t stream);
 // partial outputs between workgroups.  Used for the weights
 // gemv_rows_shape() selects (by K only, so batch and multi-weight results
 // stay those of single calls); activations plain (kXPlain), optional
-// residual.  Segments: nctas and unit_rows from gemv_rows_plan (cta_begin
-// consecutive); ws, cnt, max_range unused.
+// residual.  Segments: nctas from gemv_rows_plan (cta_begin consecutive);
+// ws, cnt, max_range unused.
 constexpr uint32_t kGemvRsMaxWaves = 8;
 // Every row-split workgroup splits all m*K activations of its wavefronts'
 // K ranges itself, so that redundant work grows with K*m; beyond 160 K
@@ -127,13 +124,9 @@ __host__ __device__ constexpr uint32_t gemv_rows_wave_lds(uint32_t m) { return 5
 // K blocks and wavefronts per workgroup the kernel accepts (a wavefront's
 // block scales sit one per lane: at most 64 blocks each).
 bool gemv_rows_shape(uint32_t kb, uint32_t waves);
-// Workgroups and rows per workgroup for one launch over weights of
-// rows[0..nseg) rows.  Weights of at least cus/2 32-row sub-tiles in all
-// run one workgroup per sub-tile (unit_rows = 32: whole 1 KiB chunks per
-// load, which the memory system streams fastest); smaller launches get cus
-// workgroups shared in proportion to the rows, each a balanced range of
-// whole 4-row quads (unit_rows = 0), so every CU streams.
-void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t cus, uint32_t *nctas, uint32_t *unit_rows);
+// Workgroups of one launch over weights of rows[0..nseg) rows: one per
+// 32-row sub-tile (whole 1 KiB chunks per load).
+void gemv_rows_plan(const uint32_t *rows, uint32_t nseg, uint32_t *nctas);
 // waves: 4 or 8; depth: ring depth 2..4 (0: by launch shape).
 hipError_t launch_gemv_rows(const GemvParams &p, uint32_t cus, uint32_t waves, uint32_t depth, hipStream_t stream);
 

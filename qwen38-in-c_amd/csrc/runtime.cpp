@@ -406,9 +406,9 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
     if (kind != kStreamK) {
         // the callers keep row-split weights on plain activations
         if (in.xmode != kXPlain) return set_error(Q35MM_EINVAL, "row-split GEMV takes plain activations");
-        uint32_t cta = 0, rows[4], nct[4], urows[4];
+        uint32_t cta = 0, rows[4], nct[4];
         for (uint32_t s = 0; s < nseg; s++) rows[s] = w[s]->w.rows;
-        gemv_rows_plan(rows, nseg, g_dev.cus, nct, urows);
+        gemv_rows_plan(rows, nseg, nct);
         for (uint32_t s = 0; s < nseg; s++) {
             const Weight &ws = w[s]->w;
             GemvSeg &g = p.seg[s];
@@ -421,7 +421,6 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
             g.nb = ws.nb;
             g.cta_begin = cta;
             g.nctas = nct[s];
-            g.unit_rows = urows[s];
             cta += g.nctas;
         }
         p.nctas = cta;
