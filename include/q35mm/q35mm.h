@@ -74,13 +74,16 @@ int q35mm_matmul(const q35mm_weight *w, uint32_t m, const float *dX, float *dY,
 /* q35mm_matmul without any allocation.  No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops).  Same dispatch, kernels and results (bit for bit)
- * as q35mm_matmul; the scratch its kernels need between launches (stream-K
- * partials and arrival counters, the GEMM's bf16 activations and K-slice
- * partials) comes from one fixed device array of 16 MiB plus 64 KiB of
- * counters that the library holds on each device until the process ends.
- * Calls that need more fail with Q35MM_EINVAL: every decode GEMV fits; a
- * GEMM fits when its bf16 activations (m rounded up to 256 rows x K x 2
- * bytes) and K-slice partials do.  q35mm_init must have run (it resolves the
+ * as q35mm_matmul, with one exception: a GEMM of at most 128 tokens whose
+ * narrow-tile K-slice partials would not fit runs on 256 x 256 tiles
+ * instead (results within the GEMM bars, not the same bits).  The scratch
+ * its kernels need between launches (stream-K partials and arrival
+ * counters, the GEMM's bf16 activations and K-slice partials) comes from
+ * one fixed device array of 16 MiB plus 64 KiB of counters that the library
+ * holds on each device until the process ends.  Calls that need more fail
+ * with Q35MM_EINVAL: every decode GEMV fits; a GEMM fits when its bf16
+ * activations (m rounded up to 256 rows x K x 2 bytes) and K-slice
+ * partials do.  q35mm_init must have run (it resolves the
  * array's address); nothing here calls an allocator.  Every call on a device
  * shares that device's array and leaves its contents behind: calls whose
  * kernels overlap on one device (different streams) race. */

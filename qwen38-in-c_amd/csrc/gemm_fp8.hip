@@ -57,6 +57,26 @@ constexpr uint32_t kBLoads = 2;    // 1 KiB pieces of B per wavefront per stage
 constexpr uint32_t kStageLoads = kALoads + kBLoads;
 static_assert(8 * kALoads * kChunkBytes == kStageA, "A pieces");
 static_assert(8 * kBLoads * kChunkBytes == kStageB, "B pieces");
+
+// Tile geometry.  The standard tile is 256 tokens x 256 weight rows; for
+// m <= 128 the narrow tile is 128 tokens x 512 rows, so a short batch does
+// not run a mostly empty 256-token tile.  Either way each of the eight
+// wavefronts computes 128 tokens x 64 rows, a stage is 48 KiB and every
+// wavefront issues six copies per stage; only the split of a stage between
+// A and B and the wavefronts' places in the tile differ.
+template <bool NARROW>
+struct GemmGeo {
+    static constexpr uint32_t kTM = NARROW ? 128 : kGemmTile;        // tokens per tile
+    static constexpr uint32_t kTR = NARROW ? 4 * 128 : kGemmTile;    // weight rows per tile
+    static constexpr uint32_t kA = kTM * kStageK * 2;                // A bytes per stage
+    static constexpr uint32_t kAL = kA / kChunkBytes / 8;            // A pieces per wavefront per stage
+    static constexpr uint32_t kBL = kTR * kStageK / kChunkBytes / 8; // B pieces per wavefront per stage
+    static constexpr uint32_t kGroups = kTR / kBlock;                // 128-row scale groups per tile
+    static constexpr uint32_t kSliceKb = 2 * kGemmMaxSliceKb / kGroups;   // scale table per group
+};
+static_assert(GemmGeo<true>::kAL + GemmGeo<true>::kBL == kStageLoads, "six copies per stage");
+static_assert(GemmGeo<true>::kA + GemmGeo<true>::kTR * kStageK == kStageBytes, "48 KiB stage");
+static_assert(GemmGeo<true>::kTM * GemmGeo<true>::kTR == kGemmTile * kGemmTile, "partial tiles of one size");
 static_assert(kGemmLds <= 160 * 1024, "LDS");
 
 // One wavefront copies 1 KiB: lane l's 16 bytes at g go to LDS l*16 past l.
@@ -381,9 +401,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     tail_tile<MULTI>(p, blockIdx.x, lds);
 }
 
-template <bool MULTI>
+template <bool MULTI, bool NARROW>
 __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     constexpr uint32_t kTM = 4, kTN = 2;   // 32x32 MFMA tiles per wavefront: 128 tokens x 64 rows
+    using Geo = GemmGeo<NARROW>;
     extern __shared__ __align__(16) uint8_t lds[];
     lds_u8 *const ring = (lds_u8 *)lds;
 
@@ -401,44 +422,46 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wm = wv & 1, wn = wv >> 1;   // 2 x 4 wavefronts of 128 x 64
+    // standard: 2 x 4 wavefronts of 128 x 64; narrow: 1 x 8
+    const uint32_t wm = NARROW ? 0 : wv & 1, wn = NARROW ? wv : wv >> 1;
 
     // ---- global sources of this wavefront's pieces ----
-    // A piece P (0..31): token rows (mt*8 + P/4)*32.., piece (h*4 + P%4) of the
-    // K block's eight (h = stage half); wavefront w copies 4w..4w+3.
-    // B piece Q (0..15): weight rows (nt*8 + Q/2)*32.., chunk 2h + Q%2;
-    // wavefront w copies 2w, 2w+1.  A missing second row group (odd NB)
-    // reads the last group instead; those columns are never stored.
+    // A piece P (0 .. 4*kTM/32 - 1): token rows (mt*kTM/32 + P/4)*32..,
+    // piece (h*4 + P%4) of the K block's eight (h = stage half); wavefront w
+    // copies pieces w*kAL ...  B piece Q: weight rows (nt*kTR/32 + Q/2)*32..,
+    // chunk 2h + Q%2; wavefront w copies w*kBL ...  A missing row group
+    // (NB not a multiple of the tile's groups) reads the last group instead;
+    // those columns are never stored.
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb);
     // Byte offsets (32-bit: the host keeps both operands under 4 GiB) that are
     // wavefront-uniform, so they live in scalar registers; each copy adds the
     // lane's 16 bytes and uses the global_load_lds saddr + voffset form.
-    uint32_t aoff[kALoads], boff[kBLoads];
+    uint32_t aoff[Geo::kAL], boff[Geo::kBL];
     const uint32_t lane16 = lane * 16;
 #pragma unroll
-    for (uint32_t i = 0; i < kALoads; i++) {
-        const uint32_t P = wv * kALoads + i;
-        aoff[i] = (mt * 8 + P / 4) * (KB * 8 * kChunkBytes) + (P % 4) * kChunkBytes;
+    for (uint32_t i = 0; i < Geo::kAL; i++) {
+        const uint32_t P = wv * Geo::kAL + i;
+        aoff[i] = (mt * (Geo::kTM / 32) + P / 4) * (KB * 8 * kChunkBytes) + (P % 4) * kChunkBytes;
     }
 #pragma unroll
-    for (uint32_t i = 0; i < kBLoads; i++) {
-        const uint32_t Q = wv * kBLoads + i;
+    for (uint32_t i = 0; i < Geo::kBL; i++) {
+        const uint32_t Q = wv * Geo::kBL + i;
         const uint32_t n32 = Q / 2;
-        const uint32_t nbk = min(nt * 2 + n32 / 4, sg.nb - 1);
+        const uint32_t nbk = min(nt * Geo::kGroups + n32 / 4, sg.nb - 1);
         boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
     }
-    // Copy k of stage st into ring slot buf: k < kALoads an A piece, then the
+    // Copy k of stage st into ring slot buf: k < kAL an A piece, then the
     // B pieces.
     auto issue_piece = [&](uint32_t st, uint32_t buf, uint32_t k) {
         const uint32_t kb = st >> 1, h = st & 1;
         lds_u8 *la = ring + buf * kStageBytes;
-        if (k < kALoads) {
+        if (k < Geo::kAL) {
             dma_1k(xa + (aoff[k] + kb * 8 * kChunkBytes + h * 4 * kChunkBytes + lane16),
-                   la + (wv * kALoads + k) * kChunkBytes);
+                   la + (wv * Geo::kAL + k) * kChunkBytes);
         } else {
-            const uint32_t i = k - kALoads;
+            const uint32_t i = k - Geo::kAL;
             dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
-                   la + kStageA + (wv * kBLoads + i) * kChunkBytes);
+                   la + Geo::kA + (wv * Geo::kBL + i) * kChunkBytes);
         }
     };
     auto issue = [&](uint32_t st, uint32_t buf) {
@@ -453,14 +476,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     // the first copy is issued, so this barrier drains nothing.
     float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
     for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
-        const uint32_t g = j / kGemmMaxSliceKb, kk = j % kGemmMaxSliceKb;
-        const uint32_t nbg = nt * 2 + g;
+        const uint32_t g = j / Geo::kSliceKb, kk = j % Geo::kSliceKb;
+        const uint32_t nbg = nt * Geo::kGroups + g;
         float v = 0.0f;
         if (nbg < sg.nb && kk < kb1 - kb0) v = sg.scale[(size_t)nbg * KB + kb0 + kk];
         sc_lds[j] = v;
     }
     __syncthreads();
-    const float *my_sc = sc_lds + (wn >> 1) * kGemmMaxSliceKb - kb0;   // indexed by kb
+    const float *my_sc = sc_lds + (wn >> 1) * Geo::kSliceKb - kb0;   // indexed by kb
     uint32_t sc_base = kb0;                                           // lane i holds block sc_base + i
     float sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
     auto scale_of = [&](uint32_t kb) {   // kb in [sc_base, sc_base + 64)
@@ -486,7 +509,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     };
     auto read_b = [&](Frags &f, uint32_t buf, uint32_t jj, uint32_t jn) {
         const uint8_t *la = lds + buf * kStageBytes;
-        f.b[jn] = *reinterpret_cast<const u32x4_t *>(la + kStageA + ((wn * kTN + jn) * 2 + jj) * kChunkBytes +
+        f.b[jn] = *reinterpret_cast<const u32x4_t *>(la + Geo::kA + ((wn * kTN + jn) * 2 + jj) * kChunkBytes +
                                                      lane * 16);
     };
     // ---- pipeline ----
@@ -640,8 +663,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
             for (uint32_t jn = 0; jn < kTN; jn++)
 #pragma unroll
                 for (uint32_t r = 0; r < 16; r++) {
-                    const uint32_t mrow = mt * kGemmTile + out_row(i, r);
-                    const uint32_t ncol = nt * kGemmTile + out_col(jn);
+                    const uint32_t mrow = mt * Geo::kTM + out_row(i, r);
+                    const uint32_t ncol = nt * Geo::kTR + out_col(jn);
                     if (mrow < p.m && ncol < sg.rows) {
                         const size_t o = (size_t)mrow * sg.ldy + ncol;
                         __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][r] : acc[i][jn][r],
@@ -651,9 +674,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         // One 64x64 tile of the last round's tail, while these stores drain
         // (every workgroup reaches this point at about the same time, when
         // the device's write bandwidth bounds the stores).
-        if (blockIdx.x < p.tail_fused) {
-            __syncthreads();   // the ring is free: every wavefront is past its last LDS read
-            tail_tile<MULTI>(p, blockIdx.x, lds);
+        if constexpr (!NARROW) {
+            if (blockIdx.x < p.tail_fused) {
+                __syncthreads();   // the ring is free: every wavefront is past its last LDS read
+                tail_tile<MULTI>(p, blockIdx.x, lds);
+            }
         }
         return;
     }
@@ -676,8 +701,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
 // One thread per float4 of a partial tile (16384 per tile); the layout is
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
 // the partials are visible without any device-scope protocol.
-template <bool MULTI>
+template <bool MULTI, bool NARROW>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+    using Geo = GemmGeo<NARROW>;
     constexpr uint32_t kTileQuads = kGemmTile * kGemmTile / 4;
     const uint32_t f = blockIdx.x * 256 + threadIdx.x;
     const uint32_t st = f / kTileQuads;                 // split tile index
@@ -701,12 +727,12 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     }
     // accumulator layout -> output coordinates (as out_row / out_col)
     const uint32_t t = fq % kGemmThreads, q = fq / kGemmThreads;
-    const uint32_t lane = t & 63, wv = t >> 6, wm = wv & 1, wn = wv >> 1;
+    const uint32_t lane = t & 63, wv = t >> 6, wm = NARROW ? 0 : wv & 1, wn = NARROW ? wv : wv >> 1;
     const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
     const TileAt ta = tile_at<MULTI>(p, tile);
     const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t row0 = ta.mt * kGemmTile + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
-    const uint32_t col = ta.nt * kGemmTile + wn * 64 + jn * 32 + (lane & 31);
+    const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+    const uint32_t col = ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
     const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
     if (col < sg.rows) {
 #pragma unroll
@@ -718,7 +744,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     }
 }
 
-GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus) {
+GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus, bool narrow) {
     // Whole rounds of tiles run unsplit; the tiles of the last, partial round
     // are cut so that round fills the device too:
     //  - into 64x64 tiles when those fit one round (gemm_tail_kernel);
@@ -730,13 +756,18 @@ GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus) {
     // slice reduction and the tail added 33 us.)
     // A K range longer than the LDS scale table (kGemmMaxSliceKb blocks)
     // splits every tile along K.
+    // Narrow tiles (m <= 128) have no 64x64 tail: their partial round is cut
+    // along K, and their scale table holds half as many K blocks per group.
     GemmPlan pl{};
-    pl.mtiles = (m + kGemmTile - 1) / kGemmTile;
+    pl.narrow = narrow;
+    const uint32_t tm = narrow ? GemmGeo<true>::kTM : GemmGeo<false>::kTM;
+    const uint32_t slice_kb = narrow ? GemmGeo<true>::kSliceKb : GemmGeo<false>::kSliceKb;
+    pl.mtiles = (m + tm - 1) / tm;
     pl.ntiles = ntiles;
     const uint32_t tiles = pl.mtiles * pl.ntiles;
     pl.tail_tile0 = tiles;
     pl.nslices = 1;
-    const uint32_t smin = (kb + kGemmMaxSliceKb - 1) / kGemmMaxSliceKb;
+    const uint32_t smin = (kb + slice_kb - 1) / slice_kb;
     if (smin > 1) {
         pl.split_tile0 = 0;
         pl.nslices = smin;
@@ -746,7 +777,7 @@ GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus) {
     const uint32_t rest = tiles - whole;
     pl.split_tile0 = tiles;
     if (!rest) return pl;
-    if (rest * kTailPerTile <= cus) {
+    if (!narrow && rest * kTailPerTile <= cus) {
         pl.split_tile0 = pl.tail_tile0 = whole;
         return pl;
     }
@@ -777,18 +808,19 @@ static bool fuse_tail() {
     return on;
 }
 
-template <bool MULTI>
+template <bool MULTI, bool NARROW>
 static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel<MULTI>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel<MULTI, NARROW>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
-        if (e == hipSuccess)
+        if (e == hipSuccess && !NARROW)
             e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel<MULTI>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTailLds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
+    if (NARROW && p.tail_tile0 != p.mtiles * p.ntiles) return hipErrorInvalidValue;   // no 64x64 tail
     const uint32_t tiles = p.mtiles * p.ntiles;
     const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
     const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
@@ -796,19 +828,23 @@ static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     GemmParams q = p;
     // the 64x64 tiles run in the whole-tile workgroups, after their stores
     q.tail_fused = (ntail && !nsplit && p.split_tile0 >= ntail && fuse_tail()) ? ntail : 0;
-    if (grid) hipLaunchKernelGGL((gemm_fp8_kernel<MULTI>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
+    if (grid)
+        hipLaunchKernelGGL((gemm_fp8_kernel<MULTI, NARROW>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
     if (nsplit) {
         const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
-        hipLaunchKernelGGL(gemm_reduce_kernel<MULTI>, dim3(quads / 256), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((gemm_reduce_kernel<MULTI, NARROW>), dim3(quads / 256), dim3(256), 0, stream, p);
     }
-    if (ntail && !q.tail_fused)
-        hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3(ntail), dim3(kGemmThreads), kTailLds, stream, q);
+    if constexpr (!NARROW) {
+        if (ntail && !q.tail_fused)
+            hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3(ntail), dim3(kGemmThreads), kTailLds, stream, q);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.nseg == 0 || p.nseg > 4) return hipErrorInvalidValue;
-    return p.nseg > 1 ? launch_gemm_t<true>(p, stream) : launch_gemm_t<false>(p, stream);
+    if (p.narrow) return p.nseg > 1 ? launch_gemm_t<true, true>(p, stream) : launch_gemm_t<false, true>(p, stream);
+    return p.nseg > 1 ? launch_gemm_t<true, false>(p, stream) : launch_gemm_t<false, false>(p, stream);
 }
 
 }  // namespace q35mm

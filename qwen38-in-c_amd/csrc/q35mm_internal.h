@@ -184,16 +184,20 @@ struct GemmParams {
     uint32_t nslices;    // K slices of each split tile (>= 2 when any tile is split)
     uint32_t tail_tile0; // first tile of the 64x64 tail (= mtiles * ntiles: none)
     uint32_t tail_fused; // 64x64 tiles run by the first whole-tile workgroups after their own tile
+    uint32_t narrow;     // tiles of 128 tokens x 512 rows (m <= 128) instead of 256 x 256
 };
 
 struct GemmPlan {
+    bool narrow;
     uint32_t mtiles, ntiles, split_tile0, nslices, tail_tile0;
     size_t ws_bytes() const {
         return nslices > 1 ? (size_t)(tail_tile0 - split_tile0) * nslices * kGemmTile * kGemmTile * 4 : 0;
     }
 };
-// ntiles: 256-row weight tiles of all segments together
-GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus);
+// ntiles: weight tiles of all segments together (256 rows, or 512 narrow)
+GemmPlan gemm_plan(uint32_t m, uint32_t ntiles, uint32_t kb, uint32_t cus, bool narrow);
+// Narrow tiles: 128 tokens x 512 weight rows, for m <= kGemmNarrowMaxM.
+constexpr uint32_t kGemmNarrowMaxM = 128, kGemmNarrowRows = 512;
 // X [m][ldx] fp32 -> lane-order bf16 [rows_pad][kb*128 cols], rows_pad a
 // multiple of 32 (m32 tiles = rows_pad / 32).  With x2: silu(x) * x2 first.
 hipError_t launch_act_to_bf16(const float *x, const float *x2, uint32_t ldx, uint32_t m, uint32_t k,

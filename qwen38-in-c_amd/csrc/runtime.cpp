@@ -105,6 +105,7 @@ struct Device {
     uint32_t done_seq = 0;
     bool done_spin = true;      // Q35MM_HOST_WAIT=sync: hipStreamSynchronize instead
     uint32_t gemm_min_m = 64;
+    bool gemm_narrow = true;    // Q35MM_GEMM_NARROW=0: 256-token tiles for every m
     uint32_t cus = 256;
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
@@ -137,6 +138,7 @@ int ensure_device() {
     HIP_TRY(noalloc_setup(dev, g_dev.stream));
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
+    g_dev.gemm_narrow = env_u32("Q35MM_GEMM_NARROW", 1) != 0;
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
     {
         const char *v = getenv("Q35MM_VERIFY_WEIGHTS");
@@ -504,7 +506,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
              hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr,
              Scratch *scr = nullptr) {
     const Weight &w0 = wt[0]->w;
-    uint32_t ntiles = 0;
+    Scratch &sc = scr ? *scr : scratch_for(st);
     for (uint32_t s = 0; s < nseg; s++) {
         const Weight &w = wt[s]->w;
         if (w.wide_scales)
@@ -512,13 +514,31 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
                              "beyond the GEMM's accumulator range (q35mm_matmul runs it on the GEMV)", w.rows, w.cols);
         if (!gemm_fits(w, m))
             return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
-        ntiles += (w.nb + 1) / 2;
     }
-    const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus);
-    const size_t xb_bytes = (size_t)pl.mtiles * kGemmTile * w0.kb * kBlock * sizeof(uint16_t);
+    // Up to 128 tokens: tiles of 128 tokens x 512 rows (4 row groups), whose
+    // partial round is cut along K -- unless those partials would not fit
+    // the fixed scratch of an allocation-free call, which then keeps the
+    // 256 x 256 tiles it always took.
+    auto plan_for = [&](bool narrow, uint32_t &groups, size_t &xb_bytes) {
+        groups = narrow ? kGemmNarrowRows / kBlock : kGemmTile / kBlock;
+        uint32_t ntiles = 0;
+        for (uint32_t s = 0; s < nseg; s++) ntiles += (wt[s]->w.nb + groups - 1) / groups;
+        const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus, narrow);
+        xb_bytes = (size_t)pl.mtiles * (narrow ? kGemmNarrowMaxM : kGemmTile) * w0.kb * kBlock * sizeof(uint16_t);
+        return pl;
+    };
+    bool narrow = m <= kGemmNarrowMaxM && g_dev.gemm_narrow;
+    uint32_t groups;
+    size_t xb_bytes;
+    GemmPlan pl = plan_for(narrow, groups, xb_bytes);
+    if (narrow && sc.fixed && ((xb_bytes + 255) & ~(size_t)255) + pl.ws_bytes() > kNoAllocBytes) {
+        narrow = false;
+        pl = plan_for(false, groups, xb_bytes);
+    }
+    const uint32_t tile_m = narrow ? kGemmNarrowMaxM : kGemmTile;
     uint16_t *xb = nullptr;
     float *ws = nullptr;
-    const int rc = scratch_gemm(scr ? *scr : scratch_for(st), xb_bytes, pl.ws_bytes(), &xb, &ws);
+    const int rc = scratch_gemm(sc, xb_bytes, pl.ws_bytes(), &xb, &ws);
     if (rc) return rc;
     GemmParams p{};
     uint32_t tile0 = 0;
@@ -533,7 +553,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         g.ldy = w.rows;
         g.nb = w.nb;
         g.tile0 = tile0;
-        tile0 += pl.mtiles * ((w.nb + 1) / 2);
+        tile0 += pl.mtiles * ((w.nb + groups - 1) / groups);
     }
     p.nseg = nseg;
     p.xb = xb;
@@ -545,7 +565,8 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.split_tile0 = pl.split_tile0;
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
-    HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (kGemmTile / kSubRows), w0.kb,
+    p.narrow = narrow ? 1u : 0u;
+    HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (tile_m / kSubRows), w0.kb,
                                xb, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;

@@ -228,13 +228,17 @@ def test_gemm_full_prefill_shapes_sampled(q, oracle, wl, gpu, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 256, 384), (100, 4700, 3000), (37, 4736, 3000), (129, 129, 129),
-                                   (300, 1000, 700), (64, 17408, 64), (513, 640, 300), (100, 512, 33000)])
+                                   (300, 1000, 700), (64, 17408, 64), (513, 640, 300), (100, 512, 33000),
+                                   (200, 256, 384), (160, 4700, 3000), (129, 17408, 64), (200, 512, 33000),
+                                   (128, 4736, 3000), (65, 17408, 5120)])
 def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
-    """Ragged m, k, n.  With at most one 256x256 tile per 16 CUs every tile
-    here runs as 64x64 tiles (gemm_tail_kernel): partial token and weight
+    """Ragged m, k, n.  Above 128 tokens (256 x 256 tiles), with at most one
+    tile per 16 CUs every tile runs as 64x64 tiles: partial token and weight
     rows, K not a multiple of 128, a K range longer than eight wavefronts'
-    share (17408), a third token tile holding one row (513).  The last
-    shape has 129 whole tiles, the last holding 232 of its 256 rows."""
+    share (17408), a third token tile holding one row (513); 200 x 33000
+    has 129 whole tiles, the last holding 232 of its 256 rows.  Up to 128
+    tokens the same shapes run the narrow 128 x 512 tiles, their partial
+    round cut into K slices (37 tokens: the GEMV)."""
     import torch
     W, sc = wl.gen_weight(m + k + n, n, k)
     X = wl.gen_act(m * k, m, k)
@@ -247,7 +251,7 @@ def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
 
 
-@pytest.mark.parametrize("m", [64, 300])
+@pytest.mark.parametrize("m", [64, 128, 300])
 def test_gemm_multi_segment(q, oracle, wl, gpu, m):
     """q35mm_matmul_multi on the GEMM path: three weights sharing K run as one
     launch over all their tiles (row counts 640, 3000 and 5000: odd row
@@ -294,11 +298,14 @@ def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
     assert (Y[:, 256:384] == 0).all()
 
 
-def test_gemm_k_beyond_one_slice_table(q, oracle, wl, gpu):
-    """K of 1025 blocks: more than one workgroup's LDS scale table, so every
-    tile is cut into two K slices and summed by the reduction kernel."""
+@pytest.mark.parametrize("m", [64, 200])
+def test_gemm_k_beyond_one_slice_table(q, oracle, wl, gpu, m):
+    """K of 1025 blocks: more than one workgroup's LDS scale table (1024
+    blocks per row group for 256 x 256 tiles, 512 for the narrow tiles of
+    m <= 128), so every tile is cut into K slices and summed by the
+    reduction kernel."""
     import torch
-    m, k, n = 64, 1025 * 128, 256
+    k, n = 1025 * 128, 256
     W, sc = wl.gen_weight(93, n, k)
     X = wl.gen_act(94, m, k, bf16=True)
     w = q.Weight(W, sc)

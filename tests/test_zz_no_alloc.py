@@ -5,6 +5,8 @@ bits.  Each case makes two calls in a row, the second with a smaller input,
 on the decode GEMV that uses scratch (stream-K: K beyond the row-split
 kernel's 160 blocks), on the row-split GEMV (no scratch) and on the prefill
 GEMM (bf16 activations and, for few tiles, K-slice partials in scratch);
+a GEMM of at most 128 tokens whose narrow-tile partials exceed the scratch
+runs on 256 x 256 tiles (within the GEMM bars of q35mm_matmul's results);
 a GEMM whose activations exceed the scratch is refused; a HIP graph of
 stream-K calls replays with the eager bits.
 """
@@ -35,8 +37,8 @@ def _both(q, w, X, m, gpu):
 
 @pytest.mark.parametrize("rows,k,ms", [(1500, 168 * 128, (5, 2)),     # stream-K GEMV
                                        (5120, 5120, (3, 1)),          # row-split GEMV
-                                       (700, 2048, (300, 96)),        # GEMM, 64x64 tail tiles
-                                       (4352, 768, (64, 64))])        # GEMM: 17 tiles x 3 K slices
+                                       (700, 2048, (300, 96)),        # GEMM: 64x64 tail tiles, then narrow tiles in K slices
+                                       (4352, 768, (64, 64))])        # GEMM: 9 narrow tiles x 3 K slices
 def test_noalloc_equals_matmul(q, oracle, wl, gpu, rows, k, ms):
     q.init()
     W, sc = wl.gen_weight(rows + k, rows, k)
@@ -52,6 +54,32 @@ def test_noalloc_equals_matmul(q, oracle, wl, gpu, rows, k, ms):
             yr = oracle.mm_batch(W, sc, Xm)
             for t in range(m):
                 assert normwise_rel(yb[t], yr[t]) <= GEMV_TOL
+    w.free()
+
+
+def test_noalloc_narrow_partials_beyond_scratch(q, oracle, wl, gpu):
+    """64 tokens x 34816 rows: q35mm_matmul cuts its 68 narrow tiles into
+    3 K slices (51 MB of partials), more than the fixed scratch holds, so the
+    allocation-free call runs the 256 x 256 tiles instead: no error, results
+    within the GEMM bars of the oracle (384 sampled columns) and of
+    q35mm_matmul's."""
+    import torch
+    q.init()
+    m, k, n = 64, 5120, 34816
+    W, sc = wl.gen_weight(21, n, k)
+    w = q.Weight(W, sc)
+    X = wl.gen_act(22, m, k, bf16=True)
+    ya, yb = _both(q, w, _dev(X, gpu), m, gpu)
+    assert np.isfinite(yb).all()
+    idx = np.sort(np.random.default_rng(23).choice(n, 384, replace=False)).astype(np.uint32)
+    idx[:2] = [0, n - 1]
+    yr = oracle.mm_rows(W, sc, X, idx)
+    for y in (ya, yb):
+        d = y[:, idx] - yr
+        rel = np.sqrt((d.astype(np.float64) ** 2).sum() / (yr.astype(np.float64) ** 2).sum())
+        assert rel <= 5e-3 and np.abs(d).max() <= 2e-2, rel
+    d = (ya - yb).astype(np.float64)
+    assert np.sqrt((d ** 2).sum() / (ya.astype(np.float64) ** 2).sum()) <= 5e-3
     w.free()
 
 
