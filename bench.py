@@ -31,8 +31,10 @@ bytes per matmul = N*K (e4m3) + 4*ceil(N/128)*ceil(K/128) (fp32 scales) +
 4*M*K (x) + 4*M*N (y).
 
 Also reported: the M=2/4/8 decode sweep, the M=512 prefill GEMM (TFLOP/s
-vs the bf16 dense MFMA peak), and the reference's own CPU path (AVX2 +
-OpenMP, oracle/_ref) timed on this host's cores on one layer at M=1.
+vs the bf16 dense MFMA peak) and the same shapes at 64 and 128 tokens
+(prefill_short: short prompts, on the narrow 128 x 512 tiles), and the
+reference's own CPU path (AVX2 + OpenMP, oracle/_ref) timed on this host's
+cores on one layer at M=1.
 """
 from __future__ import annotations
 
@@ -489,6 +491,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=100)
+    ap.add_argument("--prefill-short", type=lambda v: [int(t) for t in v.split(",") if t], default=[64, 128],
+                    help="token counts of the short-prompt prefill GEMMs timed beside M=512 (comma list; '' = none)")
     ap.add_argument("--no-blas", dest="blas", action="store_false",
                     help="skip the vendor bf16 GEMM (torch.mm -> hipBLASLt) timed beside the prefill GEMM")
     ap.add_argument("--no-mlp", dest="mlp", action="store_false",
@@ -719,6 +723,7 @@ def main():
 
     # ---- prefill GEMM at M = 512 ----
     prefill = None
+    prefill_short = {}
     if not args.no_prefill:
         prefill = {}
         for i, (name, k, n) in enumerate(wl.PREFILL_SHAPES):
@@ -736,6 +741,20 @@ def main():
                              "us": round(el_p / args.prefill_reps * 1e6, 1)}
             log(f"prefill {name}: {tf:.1f} TFLOP/s")
             del gp
+            # short prompts: the first m tokens, on the narrow 128 x 512 tiles
+            for ms in args.prefill_short:
+                Xs = X[:ms].contiguous()
+                Ys = torch.empty((ms, n), dtype=torch.float32, device=dev)
+
+                def call_s(_i, w=w, Xs=Xs, Ys=Ys):
+                    q.gemm(w, Xs, Ys)
+                el_s, gs = time_graph(torch, call_s, args.prefill_reps, 2, not args.eager)
+                prefill_short[f"{name}_m{ms}"] = {
+                    "m": ms, "k": k, "n": n, "us": round(el_s / args.prefill_reps * 1e6, 1),
+                    "TFLOPs": round(wl.flops(ms, k, n) * args.prefill_reps / el_s / 1e12, 1),
+                    "weight_GBps": round(wl.algorithmic_bytes(ms, k, n) * args.prefill_reps / el_s / 1e9, 1)}
+                log(f"prefill {name} m={ms}: {prefill_short[f'{name}_m{ms}']}")
+                del gs, Xs, Ys
             w.free()
             if args.blas:
                 # Context, not a baseline of the same op: the vendor library's
@@ -855,6 +874,7 @@ def main():
         "decode_model_token": model_token,
         "host_abi": host_abi,
         "prefill": prefill,
+        "prefill_short": prefill_short or None,
         "lm_head_bf16": lm_head,
         "mlp_block": mlp_out,
         "upload": upload,
