@@ -195,7 +195,7 @@ def test_mlp_block_real_shape(q, oracle, wl, gpu, m):
 
 @pytest.mark.parametrize("m,H,I", [(1, 640, 1664), (2, 640, 1664), (8, 5120, 1024), (13, 645, 1000),
                                    (1, 8200, 256), (1, 5120, 17408), (64, 640, 1664), (100, 645, 1000),
-                                   (1, 645, 1000), (1, 520, 1000), (1, 8192, 272)])
+                                   (1, 645, 1000), (1, 520, 1000), (1, 8192, 272), (200, 645, 1000)])
 def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
     """The block entry point gives the bits of the separate device calls it
     stands for (rmsnorm, gate+up, swiglu, down, add), whichever fusion the
@@ -229,8 +229,10 @@ def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
     assert (_host(dx2).view(np.uint32) == want.view(np.uint32)).all()
 
 
-@pytest.mark.parametrize("m", [64, 100])
+@pytest.mark.parametrize("m", [64, 100, 200])
 def test_mlp_block_prefill_path(q, oracle, wl, gpu, m):
+    """Prefill path: narrow 128 x 512 tiles cut along K up to 128 tokens
+    (the residual added in the slice sum), 256 x 256 tiles above."""
     H, I = 640, 1664
     W, dw = _mlp_weights(q, wl, H, I, wl.SEED_BASE + 0x330 + m)
     rng = np.random.default_rng(m)
