@@ -2,8 +2,8 @@
  * q35_oracle.h -- CPU restatement of the qwen35-c FP8-E4M3 128x128
  * block-scaled dequant + matmul (reference: qwen35-c/src/q35_mm.c).
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the
- * HIP implementation in qwen38-in-c_amd/.  Only tests/, the smoke check in
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle the HIP
+ * implementation in qwen38-in-c_amd/ is compared with.  Only tests/, the smoke check in
  * __graft_entry__.py and the cpu_baseline leg of bench.py may load it; the
  * product path never links, loads or falls back to it.
  *

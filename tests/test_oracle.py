@@ -1,5 +1,5 @@
 """Pins the CPU oracle (oracle/q35_oracle.c) before it is trusted as the
-parity checker of the HIP path.
+oracle the HIP path is compared with.
 
 Each part is checked against something independent of the restatement:
   - e4m3 / bf16 decode: torch's float8_e4m3fn / bfloat16 casts, the OCP

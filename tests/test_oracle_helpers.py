@@ -1,6 +1,6 @@
-"""Pins for the oracle helpers that the GPU tests use as checkers besides the
+"""Pins for the oracle helpers that the GPU tests compare with besides the
 reference-shaped entry points: the row-subset matmul (orc_mm_fp8_rows, the
-checker of the full-size prefill GEMM shapes), the fp32-scale dequant and the
+oracle of the full-size prefill GEMM shapes), the fp32-scale dequant and the
 fp32-scale batch matmul.  Each is pinned to something independent of its own
 code: the bf16-scale path (itself bit-identical to the compiled reference),
 exact rational arithmetic with one explicit rounding per reference operation

@@ -1,6 +1,6 @@
 """Pins the oracle's restatement of the MLP neighbours (RMSNorm, SiLU,
 SwiGLU, residual add; qwen35-c/src/q35_kern.c, q35_model.c:927-939) before
-it is trusted as the checker of the device kernels.
+the device kernels are compared with it.
 
 Independent checks: the reference's own fixtures (its NumPy model, with its
 test's tolerances), the FNV-1a-32 of the compiled reference's output on
