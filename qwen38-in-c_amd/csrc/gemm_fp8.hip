@@ -12,7 +12,9 @@
 //    128 (tokens) x 64 (weight rows), two per SIMD: 8 accumulators of 32x32,
 //    128 VGPRs, so the per-block rescale below is a plain v_mul.  (64 x 128
 //    wavefront tiles read 20% fewer LDS bytes per MFMA but convert twice the
-//    e4m3 codes; they ran 4% slower.)
+//    e4m3 codes; they ran 4% slower.)  Up to 128 tokens the tile is 128 x 512
+//    (the eight wavefronts side by side along the rows, same per-wavefront
+//    code), so a short batch is not three quarters padding.
 //  - K advances in stages of 64 columns (two 32-column chunks).  A stage is
 //    48 KiB of LDS: A as bf16 (32 KiB) and B still as e4m3 (16 KiB); B is
 //    widened to bf16 after the LDS read, exactly.  Stages are copied straight
