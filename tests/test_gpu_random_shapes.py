@@ -4,7 +4,8 @@ dispatch is reached at sizes the oracle finishes in about a second: the
 row-split and stream-K GEMVs, token groups of eight (9..63 tokens), the
 GEMM's narrow 128 x 512 tiles (64..128 tokens) and its 256 x 256 tiles
 above, whole tiles, K slices and 64x64 tails, K and N not multiples of 8
-or 128.
+or 128.  A second set sends 2..4 weights of random row counts through one
+q35mm_matmul_multi call.
 
 Bars as in test_gpu_parity.py: the GEMV (m < 64) within
 ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5 per token and a batch equal to its
@@ -64,3 +65,53 @@ def test_random_shape(q, oracle, wl, gpu, i, m, k, n):
         for t in (0, m - 1):
             assert (q.mm_fp8(W, sc, X[t]).view(np.uint32) == Y[t].view(np.uint32)).all(), (m, k, n, t)
     q.release(W)
+
+
+def _multi_cases(count=16, seed=20260313):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        band = i % 4
+        m = int(rng.integers(*((1, 9), (9, 64), (64, 129), (129, 257))[band]))
+        k = int(rng.integers(1, 4000))
+        if i % 2:
+            k = max(8, k // 8 * 8)
+        nseg = int(rng.integers(2, 5))
+        rows = [int(rng.integers(1, 3000)) for _ in range(nseg)]
+        cap = int(3e8 // (m * k))
+        rows = [max(1, min(r, cap // nseg)) for r in rows]
+        out.append((i, m, k, tuple(rows)))
+    return out
+
+
+@pytest.mark.parametrize("i,m,k,rows", _multi_cases())
+def test_random_multi(q, oracle, wl, gpu, i, m, k, rows):
+    """q35mm_matmul_multi over 2..4 weights of random row counts sharing K:
+    each segment within its bar of the oracle; on the GEMV the bits of a
+    single q35mm_matmul of that weight."""
+    import torch
+    gemm = m >= 64
+    Ws = [wl.gen_weight(0x3E6000 + 8 * i + s, r, k) for s, r in enumerate(rows)]
+    X = wl.gen_act(0x3E6100 + i, m, k)
+    ws = [q.Weight(W, sc) for W, sc in Ws]
+    dX = torch.from_numpy(X).to(gpu)
+    Ys = [torch.empty((m, r), dtype=torch.float32, device=gpu) for r in rows]
+    q.matmul_multi(ws, dX, Ys)
+    torch.cuda.synchronize()
+    for (W, sc), w, Y in zip(Ws, ws, Ys):
+        y = Y.cpu().numpy()
+        yr = oracle.mm_batch(W, sc, X)
+        if gemm:
+            yd, yrd = y.astype(np.float64), yr.astype(np.float64)
+            rel = np.linalg.norm(yd - yrd) / np.linalg.norm(yrd)
+            mx = np.abs(yd - yrd).max() / max(1.0, float(np.sqrt(np.mean(yrd ** 2))))
+            assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (m, k, W.shape, rel, mx)
+        else:
+            for t in range(m):
+                assert normwise_rel(y[t], yr[t]) <= GEMV_TOL, (m, k, W.shape, t)
+            single = torch.empty_like(Y)
+            q.matmul(w, dX, single)
+            torch.cuda.synchronize()
+            assert (single.cpu().numpy().view(np.uint32) == y.view(np.uint32)).all(), (m, k, W.shape)
+    for w in ws:
+        w.free()
