@@ -689,13 +689,17 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     // Stored in the accumulator layout, float4 q of thread t (q = (i*2 + jn)*4
     // + r/4) at (q*512 + t)*16 bytes of the slice's 256 KiB, so every store is
     // a coalesced 16-byte access; gemm_reduce maps it back to (row, column).
+    // A float4 holds four consecutive token rows; one whose first row is past
+    // m holds padding only and is neither stored nor read back (at m = 64 on
+    // 128-token tiles, half of every partial).
     const size_t slot = (size_t)(tile - p.split_tile0) * S + sl;
     float4 *part = reinterpret_cast<float4 *>(p.ws + slot * kGemmTile * kGemmTile);
 #pragma unroll
     for (uint32_t q = 0; q < 32; q++) {
         const uint32_t i = q / (4 * kTN), jn = (q / 4) % kTN, r4 = q & 3;
-        part[q * kGemmThreads + threadIdx.x] =
-            make_float4(acc[i][jn][4 * r4], acc[i][jn][4 * r4 + 1], acc[i][jn][4 * r4 + 2], acc[i][jn][4 * r4 + 3]);
+        if (mt * Geo::kTM + out_row(i, 4 * r4) < p.m)
+            part[q * kGemmThreads + threadIdx.x] = make_float4(acc[i][jn][4 * r4], acc[i][jn][4 * r4 + 1],
+                                                               acc[i][jn][4 * r4 + 2], acc[i][jn][4 * r4 + 3]);
     }
 }
 
@@ -712,6 +716,13 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const uint32_t fq = f - st * kTileQuads;
     const uint32_t tile = p.split_tile0 + st;
     const uint32_t S = p.nslices;
+    // accumulator layout -> output coordinates (as out_row / out_col)
+    const uint32_t t = fq % kGemmThreads, q = fq / kGemmThreads;
+    const uint32_t lane = t & 63, wv = t >> 6, wm = NARROW ? 0 : wv & 1, wn = NARROW ? wv : wv >> 1;
+    const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
+    const TileAt ta = tile_at<MULTI>(p, tile);
+    const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+    if (row0 >= p.m) return;   // padding rows: never stored by the slices
     const float4 *part = reinterpret_cast<const float4 *>(p.ws) + (size_t)st * S * kTileQuads + fq;
     float4 v[8];
     float4 tot = part[0];
@@ -727,13 +738,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
                 tot.w += v[b].w;
             }
     }
-    // accumulator layout -> output coordinates (as out_row / out_col)
-    const uint32_t t = fq % kGemmThreads, q = fq / kGemmThreads;
-    const uint32_t lane = t & 63, wv = t >> 6, wm = NARROW ? 0 : wv & 1, wn = NARROW ? wv : wv >> 1;
-    const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
-    const TileAt ta = tile_at<MULTI>(p, tile);
     const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
     const uint32_t col = ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
     const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
     if (col < sg.rows) {

@@ -253,9 +253,6 @@ int scratch_gemm(Scratch &s, size_t xb_bytes, size_t ws_bytes, uint16_t **xb, fl
 // ---------------------------------------------------------------------
 // Weight upload
 // ---------------------------------------------------------------------
-// Allocates a resident weight, lets fill() put the row-major e4m3 codes into
-// the device staging buffer raw and the fp32 block scales into w.scale
-// (asynchronously on st), then repacks raw into the lane-order tiles.
 // Allocates a resident weight and lets fill() write its lane-order tiles
 // and fp32 block scales (asynchronously on st); synchronises st.
 template <typename Fill>
