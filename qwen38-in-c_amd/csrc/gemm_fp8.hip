@@ -724,11 +724,15 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
     if (row0 >= p.m) return;   // padding rows: never stored by the slices
     const float4 *part = reinterpret_cast<const float4 *>(p.ws) + (size_t)st * S * kTileQuads + fq;
+    // Up to eight slices' loads in flight, each behind a uniform test (S is
+    // the launch's) rather than clamped to the last slice: a clamped load
+    // still costs its 16 bytes per lane of cache bandwidth.
     float4 v[8];
     float4 tot = part[0];
     for (uint32_t s0 = 1; s0 < S; s0 += 8) {
 #pragma unroll
-        for (uint32_t b = 0; b < 8; b++) v[b] = part[(size_t)min(s0 + b, S - 1) * kTileQuads];
+        for (uint32_t b = 0; b < 8; b++)
+            if (s0 + b < S) v[b] = part[(size_t)(s0 + b) * kTileQuads];
 #pragma unroll
         for (uint32_t b = 0; b < 8; b++)
             if (s0 + b < S) {
