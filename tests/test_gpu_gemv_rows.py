@@ -1,10 +1,10 @@
 """Row-split decode GEMV (gemv_rows.hip) against the oracle, through the C ABI.
 
-On a 256-CU MI355X the row-split kernel takes the weights with at least
-128 32-row sub-tiles (4065 rows) and 8..160 K blocks: the model's qkv
-(5120 -> 6144), o_proj (4096 -> 5120), gate and up (5120 -> 17408) and down
-(17408 -> 5120), which the golden cases also cover.  Above 256 sub-tiles a
-launch runs several rounds of workgroups.
+The row-split kernel takes every weight of 4..160 K blocks, one
+workgroup per 32-row sub-tile: the model's qkv (5120 -> 6144), o_proj
+(4096 -> 5120), gate and up (5120 -> 17408), down (17408 -> 5120) and its
+small projections, which the golden cases also cover.  Above 256 sub-tiles
+a launch runs several rounds of workgroups.
 Here: ragged and maximal shapes of that class, unaligned activations (the
 scalar-load staging), every token count class (1, 2, 4 or 8 tokens per
 staging layout), batch == n single calls and multi-weight == single calls
@@ -125,12 +125,11 @@ def test_mixed_matmul_multi_device_api(q, oracle, wl, gpu):
 @pytest.mark.parametrize("m,H,I", [(1, 4096, 8192), (2, 4096, 8192), (3, 4096, 8192), (8, 1024, 4096),
                                    (5, 1536, 4100), (13, 1024, 4096)])
 def test_mlp_block_all_row_split(q, oracle, wl, gpu, m, H, I):
-    """Gate and up row-split (I >= 4065 rows, 8+ K blocks; ragged rows at
-    I = 4100, two token groups at m = 13), so the RMSNorm runs as its own
-    kernel.  Down is row-split at H = 4096 (SwiGLU as its own kernel too)
-    and stream-K at H <= 1536 (SwiGLU in its staging for m <= 2); the
-    residual add stays in the down GEMV.  Checked against the oracle's block
-    and, bit for bit, against the separate calls."""
+    """Gate, up and down all row-split (8+ K blocks; ragged rows at
+    I = 4100, two token groups at m = 13): gate and up as the paired launch
+    (RMSNorm inside at one token, else its own kernel; SwiGLU inside), the
+    residual add in the down GEMV.  Checked against the oracle's block and,
+    bit for bit, against the separate calls."""
     import torch
     W = {nm: wl.gen_weight(0x400 + i, *((H, I) if nm == "down" else (I, H)))
          for i, nm in enumerate(("gate", "up", "down"))}
