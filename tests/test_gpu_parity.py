@@ -5,7 +5,8 @@ Bars (written in each test):
   - dequant and e4m3 -> bf16 conversion: bit-exact;
   - decode GEMV (fp32 path, m < 64 by default): ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5;
   - prefill GEMM (bf16 MFMA path): ||Y - Y_ref||_2 / ||Y_ref||_2 <= 5e-3 and
-    max |Y - Y_ref| <= 2e-2 on outputs of unit scale.
+    max |Y - Y_ref| <= 2e-2 on outputs of unit scale (the max divided by the
+    outputs' RMS when that exceeds 1).
 """
 import numpy as np
 import pytest
@@ -188,10 +189,14 @@ def test_zero_sizes(q):
 
 # ------------------------------------------------------------ prefill GEMM
 def _gemm_check(Y, Yr):
+    """Relative L2 error and max |Y - Y_ref| on outputs of unit scale: the
+    max is divided by the outputs' RMS when that exceeds 1 (K = 17408 with
+    weights ~N(0, 0.02) gives outputs of RMS ~2.6, whose bf16-rounding
+    errors reach 2e-2 in absolute terms at a relative L2 of 1.7e-3)."""
     Y = Y.astype(np.float64)
     Yr = Yr.astype(np.float64)
     rel = np.linalg.norm(Y - Yr) / np.linalg.norm(Yr)
-    mx = np.abs(Y - Yr).max()
+    mx = np.abs(Y - Yr).max() / max(1.0, float(np.sqrt(np.mean(Yr ** 2))))
     return rel, mx
 
 
@@ -230,7 +235,7 @@ def test_gemm_full_prefill_shapes_sampled(q, oracle, wl, gpu, k, n):
 @pytest.mark.parametrize("m,k,n", [(64, 256, 384), (100, 4700, 3000), (37, 4736, 3000), (129, 129, 129),
                                    (300, 1000, 700), (64, 17408, 64), (513, 640, 300), (100, 512, 33000),
                                    (200, 256, 384), (160, 4700, 3000), (129, 17408, 64), (200, 512, 33000),
-                                   (128, 4736, 3000), (65, 17408, 5120)])
+                                   (128, 4736, 3000), (65, 17408, 5120), (67, 5120, 4100), (258, 17408, 640)])
 def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     """Ragged m, k, n.  Above 128 tokens (256 x 256 tiles), with at most one
     tile per 16 CUs every tile runs as 64x64 tiles: partial token and weight
@@ -238,7 +243,9 @@ def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     share (17408), a third token tile holding one row (513); 200 x 33000
     has 129 whole tiles, the last holding 232 of its 256 rows.  Up to 128
     tokens the same shapes run the narrow 128 x 512 tiles, their partial
-    round cut into K slices (37 tokens: the GEMV)."""
+    round cut into K slices (37 tokens: the GEMV).  The slices skip the
+    float4s of padding token rows: 65 and 67 tokens end inside a float4,
+    and 258 x 17408 x 640 slices a second token tile of two rows."""
     import torch
     W, sc = wl.gen_weight(m + k + n, n, k)
     X = wl.gen_act(m * k, m, k)
