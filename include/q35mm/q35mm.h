@@ -192,6 +192,24 @@ void q35mm_release_all(void);
 /* Frees every device resource of the library. */
 void q35mm_shutdown(void);
 
+/* Scratch of one stream.  Each stream the device API is called on gets its
+ * own scratch set (split partials, counters, staged activations, the MLP
+ * block's intermediates: tens to hundreds of MB at prefill sizes), kept
+ * until this call or q35mm_shutdown.  A caller that creates and destroys
+ * streams calls it before destroying one (after waiting for the device).
+ * A set that a captured HIP graph used is never freed before
+ * q35mm_shutdown, so graphs stay valid: its buffers are moved aside instead.
+ * No counterpart in the reference (its calls keep no state). */
+int q35mm_stream_release(void *stream);
+
+/* Debug: after waiting for the device, the number of nonzero words among
+ * the arrival counters of `stream`'s scratch (noalloc = 0) or of the
+ * allocation-free entry point's fixed scratch (noalloc = 1), and how many
+ * words there are.  Every launch returns the counters it takes to zero, so
+ * both read 0 nonzero words between calls.  No counterpart in the
+ * reference. */
+int q35mm_debug_counters(void *stream, int noalloc, uint64_t *nonzero, uint64_t *words);
+
 const char *q35mm_last_error(void);
 
 /* Number of resident copies the drop-in entry points currently hold. */

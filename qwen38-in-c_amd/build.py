@@ -4,9 +4,7 @@
     python qwen38-in-c_amd/build.py --asm    # also dump device assembly to _build/
 
 The library is written to qwen38-in-c_amd/lib/libq35mm.so; tests, the
-benchmark and the smoke check load it from there.  The ceiling probe
-(probes/q35mm_probe.hip: raw weight-read rate, MFMA issue rate) is built
-beside it as lib/q35mm_probe.
+benchmark and the smoke check load it from there.
 """
 from __future__ import annotations
 
@@ -32,41 +30,38 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
-def build_library(verbose: bool = False) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *DEVICE_FLAGS, *COMMON_FLAGS, "-shared", "-Wl,-Bsymbolic-functions", "-o", tmp, *sources()]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> list[str]:
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 target feature and says so.
     noise = ("packed-fp32-ops", "is not a recognized feature", "warning: argument unused")
     msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if ln.strip() and not any(n in ln for n in noise)]
     if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + "\n".join(msgs))
+    return msgs
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compiles every source to an object (in parallel) under _build/obj,
+    then links lib/libq35mm.so."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    objdir = os.path.join(ROOT, "_build", "obj")
+    os.makedirs(objdir, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(objdir, os.path.basename(s) + ".o") for s in srcs]
+    cmds = [[HIPCC, *DEVICE_FLAGS, *COMMON_FLAGS, "-c", "-o", o, s] for s, o in zip(srcs, objs)]
+    if verbose:
+        for c in cmds:
+            print(" ".join(c), flush=True)
+    from concurrent.futures import ThreadPoolExecutor
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(jobs) as ex:
+        msgs = [m for ms in ex.map(_run, cmds) for m in ms]
+    tmp = LIB + ".tmp"
+    msgs += _run([HIPCC, *DEVICE_FLAGS, "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", "-o", tmp, *objs])
     if msgs and verbose:
         print("\n".join(msgs))
     os.replace(tmp, LIB)
     return LIB
-
-
-PROBE_SRC = os.path.join(PKG, "probes", "q35mm_probe.hip")
-PROBE = os.path.join(LIBDIR, "q35mm_probe")
-
-
-def build_probe(verbose: bool = False) -> str:
-    """The ceiling probe (raw weight reads, MFMA issue rate): a separate
-    executable, not part of the library."""
-    os.makedirs(LIBDIR, exist_ok=True)
-    tmp = PROBE + ".tmp"
-    cmd = [HIPCC, *DEVICE_FLAGS, "-O3", "-std=c++17", "-o", tmp, PROBE_SRC]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed on the probe:\n" + res.stdout + res.stderr)
-    os.replace(tmp, PROBE)
-    return PROBE
 
 
 def dump_asm(outdir: str) -> None:
@@ -79,6 +74,5 @@ def dump_asm(outdir: str) -> None:
 
 if __name__ == "__main__":
     print(build_library(verbose=True))
-    print(build_probe())
     if "--asm" in sys.argv:
         dump_asm(os.path.join(ROOT, "_build", "asm"))

@@ -134,11 +134,22 @@ __device__ __forceinline__ void stage_finish(float (&xv)[8], const StageIn<XM> &
     }
 }
 
+// SHIFT: the workgroup's range holds a wide value (kActWide): every staged
+// value is multiplied by kActShift and the block scales by kActUnshift.
+template <bool SHIFT>
 __device__ __forceinline__ void stage_store(uint8_t *lds, uint32_t m, const StageItem &it, const float (&xv)[8]) {
     const uint32_t R = stage_rows(m);
     uint32_t p0[4], p1[4], p2[4];   // packed pairs of columns
 #pragma unroll
-    for (int e = 0; e < 4; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], p0[e], p1[e], p2[e]);
+    for (int e = 0; e < 4; e++) {
+        if constexpr (SHIFT) {
+            const float a = xv[2 * e] * kActShift, b = xv[2 * e + 1] * kActShift;
+            split3_bf16x2(a, b, p0[e], p1[e], p2[e]);
+            split3_fix_inf(p0[e], p1[e], p2[e]);
+        } else {
+            split3_bf16x2(xv[2 * e], xv[2 * e + 1], p0[e], p1[e], p2[e]);
+        }
+    }
     const uint32_t c = it.kk >> 5, h = (it.kk >> 4) & 1, q = (it.kk >> 3) & 1;
     const uint32_t base = (c * 2 + q) * R;
     const u32x4_t w0 = {p0[0], p0[1], p0[2], p0[3]};
@@ -321,14 +332,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
         ring_prologue();
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Split and stage while the weight blocks are in flight.
+    // Split and stage while the weight blocks are in flight.  wide: a
+    // staged value of this thread reached kActWide.
+    bool wide = false;
 #pragma unroll
     for (uint32_t u = 0; u < kStagePre; u++) {
         const uint32_t i = threadIdx.x + u * kGemvThreads;
         const StageItem it = stage_item(min(i, nvec - 1), per_t, KB, b0);
         float xv[8];
         stage_finish(xv, xpre[u], p.k, it, s_inv);
-        if (i < nvec) stage_store(lds, M, it, xv);
+        if (i < nvec) {
+            wide |= max_abs(xv) >= kActWide;
+            stage_store<false>(lds, M, it, xv);
+        }
     }
     // The rest (m > 1) in batches of kStageBatch items per thread: the loads
     // of a batch are all issued before any is used (the scheduling barrier
@@ -346,11 +362,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_fp8_kernel(GemvParams p) {
             const StageItem it = stage_item(min(i, nvec - 1), per_t, KB, b0);
             float xv[8];
             stage_finish(xv, in[u], p.k, it, s_inv);
-            if (i < nvec) stage_store(lds, M, it, xv);
+            if (i < nvec) {
+                wide |= max_abs(xv) >= kActWide;
+                stage_store<false>(lds, M, it, xv);
+            }
         }
     }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + zero_off)[threadIdx.x] = 0u;
-    __syncthreads();
+    if (__builtin_expect(__syncthreads_or(wide), 0)) {
+        // Rare: the range holds a wide value or an infinity.  Stage it all
+        // again, shifted, and take the block scales times kActUnshift.
+        for (uint32_t i = threadIdx.x; i < nvec; i += kGemvThreads) {
+            const StageItem it = stage_item(i, per_t, KB, b0);
+            StageIn<XM> in;
+            stage_load<XM, VEC>(in, p, it);
+            float xv[8];
+            stage_finish(xv, in, p.k, it, s_inv);
+            stage_store<true>(lds, M, it, xv);
+        }
+        sc_lane *= kActUnshift;
+        __syncthreads();
+    }
 
     f32x16_t acc = {};
     const f32x16_t zero = {};

@@ -121,12 +121,14 @@ __device__ __forceinline__ void load_xblock(XBlock<MT> &xb, const float *x, uint
 // A lane writes its share of those 16-byte units: per part 4 bytes (G = 2)
 // or 8 bytes per group of four columns.  Columns >= k are staged as zero;
 // only a partial last block (a wavefront-uniform test) pays for the masks.
+// Returns (the same for every lane) whether the block holds a wide value
+// and was staged multiplied by kActShift: its scale is then taken times
+// kActUnshift.
 template <uint32_t MT>
-__device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot, uint32_t m, uint32_t R, uint32_t k,
+__device__ __forceinline__ bool stage_xblock(const XBlock<MT> &xb, uint8_t *slot, uint32_t m, uint32_t R, uint32_t k,
                                              uint32_t kb, uint32_t lane) {
     constexpr uint32_t G = XBlock<MT>::kG;
     const uint32_t t = lane / XBlock<MT>::kLanesPerToken;
-    if (t >= m) return;
     float xv[G];
 #pragma unroll
     for (uint32_t e = 0; e < G; e++) xv[e] = xb.v[e];
@@ -134,9 +136,19 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
 #pragma unroll
         for (uint32_t e = 0; e < G; e++) xv[e] = kb * kBlock + xcol<MT>(lane, e) < k ? xb.v[e] : 0.0f;
     }
+    const bool wide = __builtin_amdgcn_ballot_w64(t < m && max_abs(xv) >= kActWide) != 0;
+    if (t >= m) return wide;
+    if (__builtin_expect(wide, 0)) {
+#pragma unroll
+        for (uint32_t e = 0; e < G; e++) xv[e] *= kActShift;
+    }
     uint32_t pr[3][G / 2];   // per part, packed bf16 pairs
 #pragma unroll
     for (uint32_t e = 0; e < G / 2; e++) split3_bf16x2(xv[2 * e], xv[2 * e + 1], pr[0][e], pr[1][e], pr[2][e]);
+    if (__builtin_expect(wide, 0)) {
+#pragma unroll
+        for (uint32_t e = 0; e < G / 2; e++) split3_fix_inf(pr[0][e], pr[1][e], pr[2][e]);
+    }
 #pragma unroll
     for (uint32_t part = 0; part < 3; part++) {
         const uint32_t ai = part * m + t;
@@ -151,6 +163,15 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
                 *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pr[part][2 * i], pr[part][2 * i + 1]};
         }
     }
+    return wide;
+}
+
+// Wavefronts per SIMD the register allocator must leave room for: four
+// (128 registers, accumulators included) for one token on a ring of two
+// blocks -- the gate+up launch, several rounds of workgroups -- which the
+// plain kernel fits; the rest as many as their registers allow.
+constexpr uint32_t rows_min_waves(uint32_t mt, uint32_t depth, uint32_t nw) {
+    return mt == 1 && depth == 2 && nw == 4 ? 4 : 1;
 }
 
 }  // namespace
@@ -160,7 +181,8 @@ __device__ __forceinline__ void stage_xblock(const XBlock<MT> &xb, uint8_t *slot
 // kRowsPair -- the MLP's gate (segment 0) and up (segment 1) together,
 // writing silu(gate) * up; kRowsPairNorm -- the same on RMSNorm(x).
 template <bool VEC, uint32_t MT, uint32_t DEPTH, uint32_t NW, uint32_t MODE = kRowsPlain>
-__global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(rows_min_waves(MT, DEPTH, NW), 8)))
+void gemv_rows_kernel(GemvParams p) {
     constexpr bool PAIR = MODE != kRowsPlain, NORM = MODE == kRowsPairNorm;
     static_assert(!NORM || MT == 1, "the fused RMSNorm is for one token");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -282,7 +304,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
 #pragma unroll
         for (uint32_t e = 0; e < XBlock<MT>::kG; e++) x0.v[e] = rmsnorm1(x0.v[e], inv, w0.v[e]);
     }
-    stage_xblock<MT>(x0, wbase, M, R, p.k, kbof(0), lane);   // waits for x0 only: loads complete in order
+    // A block staged shifted (wide activations) takes its scale times
+    // kActUnshift: lane i holds block i's scales, so only that lane changes.
+    float sca_l = sca_lane, scb_l = scb_lane;
+    auto unshift_scale = [&](uint32_t i) {
+        if (lane == i) {
+            sca_l *= kActUnshift;
+            scb_l *= kActUnshift;
+        }
+    };
+    // waits for x0 only: loads complete in order
+    if (__builtin_expect(stage_xblock<MT>(x0, wbase, M, R, p.k, kbof(0), lane), 0)) unshift_scale(0);
 
     // ---- stream ----
     f32x16_t acc = {};
@@ -304,7 +336,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
 #pragma unroll
                     for (uint32_t e = 0; e < XBlock<MT>::kG; e++) xr[d].v[e] = rmsnorm1(xr[d].v[e], inv, wr[d].v[e]);
                 }
-                if (bb + 1 < n) stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, kbof(bb + 1), lane);
+                if (bb + 1 < n &&
+                    __builtin_expect(stage_xblock<MT>(xr[d], wbase + (par ^ 1) * 256 * R, M, R, p.k, kbof(bb + 1), lane), 0))
+                    unshift_scale(bb + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16_t part;
 #pragma unroll
@@ -316,9 +350,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_kernel(GemvParams p) {
                         part = mfma32x32x16(aop, bop, (j == 0 && q == 0) ? zero : part);
                     }
                 const float sca =
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sca_lane), bb));
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sca_l), bb));
                 const float scb =
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scb_lane), bb));
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scb_l), bb));
                 const float sc = out_in_a ? sca : scb;
                 // acc[r + 4p] holds part p of token 4h + (r & 3): only tokens
                 // below MT are scaled; rows 24..31 carry nothing (regs 12..15)

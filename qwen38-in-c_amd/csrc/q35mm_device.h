@@ -80,7 +80,8 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return bits_f32(b << 
 // Exact three-way split of two fp32 values into bf16 parts, packed in pairs:
 // x == p0 + p1 + p2 for every normal x (each residual is exact in fp32 and has
 // at most 16, then 8, significant bits).  Each part is a round-to-nearest-even
-// conversion; about 5.5 instructions per value.
+// conversion; about 5.5 instructions per value.  Blocks holding wide values
+// or infinities are shifted first and fixed up by split3_fix_inf (below).
 __device__ __forceinline__ void split3_bf16x2(float a, float b, uint32_t &p0, uint32_t &p1, uint32_t &p2) {
 #pragma clang fp contract(off)
     const f32x2v_t x = {a, b};
@@ -91,6 +92,43 @@ __device__ __forceinline__ void split3_bf16x2(float a, float b, uint32_t &p0, ui
     p0 = __builtin_bit_cast(uint32_t, b0);
     p1 = __builtin_bit_cast(uint32_t, b1);
     p2 = __builtin_bit_cast(uint32_t, __builtin_convertvector(r2, bf16x2v_t));
+}
+
+// Wide activations.  A K block's raw partial sum_k x_k * code_k (codes up
+// to +-448, 128 terms) can overflow fp32 once |x| reaches ~2^112, where the
+// reference's products (code * scale) * x stay finite.  A block (row-split
+// GEMV) or a workgroup's range (stream-K) holding a value of magnitude
+// kActWide or more is therefore staged multiplied by kActShift, and its
+// block scales are taken multiplied by kActUnshift: both factors are powers
+// of two, so fmaf(scale * 2^64, part * 2^-64, acc) rounds exactly as
+// fmaf(scale, part, acc) would, and the bits are those of the plain path
+// (values below 2^-62 in magnitude in such a block lose bits as subnormals).
+// NaN is ignored by the test (every part of a NaN is NaN, and the output is
+// NaN as the reference's fmaf chain gives it).
+constexpr float kActWide = 0x1.0p96f;
+constexpr float kActShift = 0x1.0p-64f;
+constexpr float kActUnshift = 0x1.0p64f;
+
+// After split3_bf16x2 of two values of a shifted block (finite values are
+// below 2^64 there and split exactly): an infinity passes whole in part 0
+// with zero residuals, so inf * w gives +-inf (NaN for w = 0), as
+// fmaf(w, x, acc) does (qwen35-c/src/q35_mm.c:110-111) -- the plain split
+// forms inf - inf = NaN in the residuals.  In a shifted block part 0 is a
+// bf16 infinity exactly when the value is one, so the test reads part 0.
+__device__ __forceinline__ void split3_fix_inf(uint32_t p0, uint32_t &p1, uint32_t &p2) {
+    const uint32_t keep = ((p0 & 0x7FFFu) == 0x7F80u ? 0xFFFF0000u : 0xFFFFFFFFu) &
+                          ((p0 & 0x7FFF0000u) == 0x7F800000u ? 0x0000FFFFu : 0xFFFFFFFFu);
+    p1 &= keep;
+    p2 &= keep;
+}
+
+// Largest |x| of n values (NaN ignored): v_max3_f32 with abs modifiers.
+template <uint32_t N>
+__device__ __forceinline__ float max_abs(const float (&v)[N]) {
+    float mx = 0.0f;
+#pragma unroll
+    for (uint32_t e = 0; e < N; e++) mx = __builtin_fmaxf(mx, __builtin_fabsf(v[e]));
+    return mx;
 }
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {

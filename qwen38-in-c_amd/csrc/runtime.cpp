@@ -88,6 +88,14 @@ struct Scratch {
     // Set for q35mm_matmul_noalloc: the device address of the fixed scratch
     // array (noalloc.hip); nothing is allocated, oversized requests fail.
     uint8_t *fixed = nullptr;
+    // Set once a call captured into a HIP graph used this set: the graph
+    // holds its buffers' addresses, so from then on they are never freed
+    // before q35mm_shutdown -- growth allocates new buffers and retires the
+    // old ones (a replay after a free would write into memory that may by
+    // then belong to anything else, another stream's counters included).
+    bool captured = false;
+    // The current call's stream is being captured: it cannot allocate.
+    bool capturing = false;
 };
 
 struct Device {
@@ -95,6 +103,7 @@ struct Device {
     hipStream_t stream = nullptr;
     std::unordered_map<hipStream_t, Scratch> scratch;
     Scratch *last_scratch = nullptr;   // of the most recent call outside graph capture
+    std::vector<void *> retired;       // buffers a captured graph may still use (freed at shutdown)
     DevBuf dx, dy;    // activation staging for the host-pointer ABI
     void *up_pin[4] = {};        // pinned chunks of the file -> HBM upload ring
     void *up_dev[4] = {};        // device side of each chunk (+ room for its codes)
@@ -165,28 +174,47 @@ hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 // into a graph cannot allocate: it shares the scratch of the most recent
 // call made outside capture (its warm-up, in the usual capture pattern), so
 // such a graph and eager work on that stream must not run at the same time.
+// A set used under capture is marked captured (its buffers are never freed
+// before q35mm_shutdown, see Scratch).
 Scratch &scratch_for(hipStream_t st) {
-    auto it = g_dev.scratch.find(st);
-    if (it == g_dev.scratch.end()) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (g_dev.last_scratch && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return *g_dev.last_scratch;
-        it = g_dev.scratch.emplace(st, Scratch()).first;
-    }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) g_dev.last_scratch = &it->second;
-    return it->second;
+    const bool capturing = hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    Scratch *s = nullptr;
+    auto it = g_dev.scratch.find(st);
+    if (it != g_dev.scratch.end())
+        s = &it->second;
+    else if (capturing && g_dev.last_scratch)
+        s = g_dev.last_scratch;
+    else
+        s = &g_dev.scratch.emplace(st, Scratch()).first->second;
+    s->capturing = capturing;
+    if (capturing)
+        s->captured = true;
+    else
+        g_dev.last_scratch = s;
+    return *s;
 }
 
-
 // Grows a device buffer; waits for the device first because kernels queued
-// on any stream may still use the old allocation.
-int grow(DevBuf &b, size_t bytes, bool zero) {
+// on any stream may still use the old allocation.  owner: the scratch set
+// the buffer belongs to (null for the host-pointer ABI's own buffers): under
+// capture nothing can be allocated, and a set a graph has captured keeps its
+// old buffer alive (retired) instead of freeing it.
+int grow(DevBuf &b, size_t bytes, bool zero, Scratch *owner = nullptr) {
     if (b.cap >= bytes) return Q35MM_OK;
+    if (owner && owner->capturing)
+        return set_error(Q35MM_EINVAL, "%zu bytes of scratch needed while the stream is being captured into a "
+                         "graph (%zu available): a capture cannot allocate -- make the same call once outside "
+                         "capture first", bytes, b.cap);
     size_t cap = std::max(bytes, b.cap * 2);
     cap = (cap + 4095) & ~(size_t)4095;
     HIP_TRY(hipDeviceSynchronize());
-    if (b.ptr) HIP_TRY(hipFree(b.ptr));
+    if (b.ptr) {
+        if (owner && owner->captured)
+            g_dev.retired.push_back(b.ptr);
+        else
+            HIP_TRY(hipFree(b.ptr));
+    }
     b.ptr = nullptr;
     b.cap = 0;
     if (hipMalloc(&b.ptr, cap) != hipSuccess) {
@@ -223,8 +251,8 @@ int scratch_splitk(Scratch &s, size_t ws_bytes, size_t cnt_bytes, float **ws, ui
         *ws = reinterpret_cast<float *>(s.fixed + kNoAllocCntBytes);
         return Q35MM_OK;
     }
-    int rc = grow(s.ws, ws_bytes, false);
-    if (!rc) rc = grow(s.cnt, cnt_bytes, true);
+    int rc = grow(s.ws, ws_bytes, false, &s);
+    if (!rc) rc = grow(s.cnt, cnt_bytes, true, &s);
     if (rc) return rc;
     *ws = (float *)s.ws.ptr;
     *cnt = (uint32_t *)s.cnt.ptr;
@@ -242,8 +270,8 @@ int scratch_gemm(Scratch &s, size_t xb_bytes, size_t ws_bytes, uint16_t **xb, fl
         *ws = reinterpret_cast<float *>(s.fixed + kNoAllocCntBytes + xb_al);
         return Q35MM_OK;
     }
-    int rc = grow(s.xb, xb_bytes, false);
-    if (!rc && ws_bytes) rc = grow(s.ws, ws_bytes, false);
+    int rc = grow(s.xb, xb_bytes, false, &s);
+    if (!rc && ws_bytes) rc = grow(s.ws, ws_bytes, false, &s);
     if (rc) return rc;
     *xb = (uint16_t *)s.xb.ptr;
     *ws = (float *)s.ws.ptr;
@@ -1349,7 +1377,7 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
     const size_t nh = (size_t)m * H, ni = (size_t)m * I;
     hipStream_t st = pick_stream(stream);
     Scratch &scr = scratch_for(st);
-    rc = grow(scr.mlp, (2 * nh + 2 * ni) * sizeof(float), false);
+    rc = grow(scr.mlp, (2 * nh + 2 * ni) * sizeof(float), false, &scr);
     if (rc) return rc;
     float *xn = (float *)scr.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     const bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(gate->w, m) &&
@@ -1552,6 +1580,8 @@ Q35MM_API void q35mm_shutdown(void) {
             if (b->ptr) (void)hipFree(b->ptr);
     g_dev.scratch.clear();
     g_dev.last_scratch = nullptr;
+    for (void *ptr : g_dev.retired) (void)hipFree(ptr);
+    g_dev.retired.clear();
     for (DevBuf *b : {&g_dev.dx, &g_dev.dy}) {
         if (b->ptr) (void)hipFree(b->ptr);
         b->ptr = nullptr;
@@ -1573,6 +1603,55 @@ Q35MM_API void q35mm_shutdown(void) {
     if (g_dev.stream) (void)hipStreamDestroy(g_dev.stream);
     g_dev.stream = nullptr;
     g_dev.id = -1;
+}
+
+Q35MM_API int q35mm_stream_release(void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (g_dev.id < 0) return Q35MM_OK;
+    auto it = g_dev.scratch.find(pick_stream(stream));
+    if (it == g_dev.scratch.end()) return Q35MM_OK;
+    HIP_TRY(hipDeviceSynchronize());
+    Scratch &s = it->second;
+    for (DevBuf *b : {&s.ws, &s.cnt, &s.xb, &s.mlp}) {
+        if (!b->ptr) continue;
+        if (s.captured)
+            g_dev.retired.push_back(b->ptr);   // a captured graph may still replay into it
+        else
+            HIP_TRY(hipFree(b->ptr));
+        b->ptr = nullptr;
+        b->cap = 0;
+    }
+    if (g_dev.last_scratch == &s) g_dev.last_scratch = nullptr;
+    g_dev.scratch.erase(it);
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_debug_counters(void *stream, int noalloc, uint64_t *nonzero, uint64_t *words) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (nonzero) *nonzero = 0;
+    if (words) *words = 0;
+    if (g_dev.id < 0) return Q35MM_OK;
+    HIP_TRY(hipDeviceSynchronize());
+    const uint32_t *src = nullptr;
+    size_t n = 0;
+    if (noalloc) {
+        src = reinterpret_cast<const uint32_t *>(noalloc_scratch(g_dev.id));
+        n = src ? kNoAllocCntBytes / sizeof(uint32_t) : 0;
+    } else {
+        auto it = g_dev.scratch.find(pick_stream(stream));
+        if (it != g_dev.scratch.end() && it->second.cnt.ptr) {
+            src = static_cast<const uint32_t *>(it->second.cnt.ptr);
+            n = it->second.cnt.cap / sizeof(uint32_t);
+        }
+    }
+    if (!n) return Q35MM_OK;
+    std::vector<uint32_t> h(n);
+    HIP_TRY(hipMemcpy(h.data(), src, n * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    uint64_t nz = 0;
+    for (uint32_t v : h) nz += v != 0;
+    if (nonzero) *nonzero = nz;
+    if (words) *words = n;
+    return Q35MM_OK;
 }
 
 Q35MM_API const char *q35mm_last_error(void) { return t_last_error.c_str(); }

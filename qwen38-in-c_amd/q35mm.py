@@ -106,6 +106,8 @@ def _load(path: str = LIB_PATH) -> C.CDLL:
     lib.q35mm_shutdown.restype = None
     lib.q35mm_last_error.restype = C.c_char_p
     lib.q35mm_resident_count.restype = C.c_size_t
+    lib.q35mm_stream_release.argtypes = [vp]
+    lib.q35mm_debug_counters.argtypes = [vp, C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
     return lib
 
 
@@ -435,3 +437,18 @@ def free(dptr: int) -> None:
 
 def shutdown() -> None:
     lib.q35mm_shutdown()
+
+
+def stream_release(stream=None) -> None:
+    """q35mm_stream_release: free the scratch of a stream (default: torch's
+    current stream) before it is destroyed."""
+    _check(lib.q35mm_stream_release(_stream(stream)), "q35mm_stream_release")
+
+
+def debug_counters(stream=None, noalloc: bool = False) -> tuple[int, int]:
+    """q35mm_debug_counters: (nonzero words, words) among the arrival
+    counters of a stream's scratch, or of the allocation-free scratch."""
+    nz, n = C.c_uint64(), C.c_uint64()
+    _check(lib.q35mm_debug_counters(_stream(stream), 1 if noalloc else 0, C.byref(nz), C.byref(n)),
+           "q35mm_debug_counters")
+    return int(nz.value), int(n.value)

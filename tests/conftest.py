@@ -117,6 +117,16 @@ def goldens():
     return json.load(open(os.path.join(GOLDEN, "ref_hashes.json")))
 
 
+def unit_scale_act(X, k: int, std: float = 0.02):
+    """X times the power of two 2^-e, e = max(0, ceil(log2(std * sqrt(k)))):
+    with weights ~N(0, std^2), outputs of K = k terms then have an RMS of at
+    most 1, the scale the GEMM's absolute max-error bar is stated for.  The
+    factor is exact (bf16-representable activations stay so) and leaves every
+    relative error unchanged."""
+    e = max(0, int(np.ceil(np.log2(std * np.sqrt(k)))))
+    return np.ascontiguousarray(X * np.float32(2.0 ** -e)) if e else X
+
+
 def normwise_rel(y, yref) -> float:
     """||y - yref||_inf / ||yref||_inf in float64."""
     y = np.asarray(y, np.float64)

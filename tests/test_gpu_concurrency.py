@@ -74,6 +74,13 @@ def test_two_streams_overlap(q, oracle, wl, gpu):
     for y1, g1, y2, g2 in outs:
         for got, name in ((y1, "a"), (g1, "g1"), (y2, "b"), (g2, "g2")):
             assert (got.cpu().numpy().view(np.uint32) == ref[name].view(np.uint32)).all(), name
+    # every stream-K launch returned the arrival counters it took to zero
+    for st in (s1, s2, torch.cuda.current_stream()):
+        nz, words = q.debug_counters(st.cuda_stream)
+        assert words > 0 and nz == 0, (nz, words)
+    for st in (s1, s2):
+        q.stream_release(st.cuda_stream)
+        assert q.debug_counters(st.cuda_stream) == (0, 0)
     for w in (wa, wb, wg):
         w.free()
 
@@ -168,4 +175,83 @@ def test_graph_captured_on_a_fresh_stream(q, wl, gpu):
         q.gemm(w, X[:64], other)
         torch.cuda.synchronize()
     del g
+    w.free()
+
+
+def test_graph_replays_after_its_scratch_grew(q, wl, gpu):
+    """A graph captured on a fresh stream keeps the addresses of the scratch
+    it borrowed from the warm-up stream.  An eager call with more tokens on
+    that stream then needs larger buffers: the set, marked as captured,
+    retires its old buffers instead of freeing them, so every replay still
+    gives the eager bits (a freed buffer could by then belong to anything,
+    another set's counters included).  The counters read zero throughout."""
+    import torch
+    W, sc = wl.gen_weight(341, 700, 2048)
+    w = q.Weight(W, sc)
+    cur = torch.cuda.current_stream()
+    q.stream_release(cur.cuda_stream)       # start from an empty set on this stream
+    X = _dev(wl.gen_act(342, 96, 2048), gpu)
+    want = torch.empty((96, 700), device=gpu)
+    q.gemm(w, X, want)                      # warm-up: the set holds 96 tokens' worth
+    torch.cuda.synchronize()
+    Y = torch.empty_like(want)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(cur)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            q.gemm(w, X, Y)
+    torch.cuda.synchronize()
+    Xb = _dev(wl.gen_act(343, 512, 2048), gpu)
+    big = torch.empty((512, 700), device=gpu)
+    for r, m in enumerate((256, 512, 512)):   # the set grows on the first two rounds
+        Y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert (Y.cpu().numpy().view(np.uint32) == want.cpu().numpy().view(np.uint32)).all(), r
+        q.gemm(w, Xb[:m], big[:m])
+        torch.cuda.synchronize()
+        assert q.debug_counters(cur.cuda_stream)[0] == 0
+    del g
+    w.free()
+
+
+def test_capture_cannot_grow_scratch(q, wl, gpu):
+    """A call that would need more scratch than the set a capture borrows
+    is refused with a clear error before it launches anything (a capture
+    cannot allocate); the same call made once outside capture first then
+    captures and replays with the eager bits."""
+    import torch
+    W, sc = wl.gen_weight(351, 700, 2048)
+    w = q.Weight(W, sc)
+    cur = torch.cuda.current_stream()
+    q.stream_release(cur.cuda_stream)
+    X = _dev(wl.gen_act(352, 300, 2048), gpu)
+    small = torch.empty((64, 700), device=gpu)
+    q.gemm(w, X[:64], small)                # warm-up with fewer tokens than the capture
+    torch.cuda.synchronize()
+    Y = torch.empty((300, 700), device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(cur)
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(q.Q35mmError, match="captured into a graph"):
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                q.gemm(w, X, Y)
+    torch.cuda.synchronize()
+    want = torch.empty_like(Y)
+    q.gemm(w, X, want)                      # the warm-up the capture needs
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    s2 = torch.cuda.Stream()
+    s2.wait_stream(cur)
+    with torch.cuda.stream(s2):
+        with torch.cuda.graph(g2, stream=s2):
+            q.gemm(w, X, Y)
+    for r in range(2):
+        Y.fill_(float("nan"))
+        g2.replay()
+        torch.cuda.synchronize()
+        assert (Y.cpu().numpy().view(np.uint32) == want.cpu().numpy().view(np.uint32)).all(), r
+    del g, g2
     w.free()

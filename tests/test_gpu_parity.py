@@ -5,13 +5,14 @@ Bars (written in each test):
   - dequant and e4m3 -> bf16 conversion: bit-exact;
   - decode GEMV (fp32 path, m < 64 by default): ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5;
   - prefill GEMM (bf16 MFMA path): ||Y - Y_ref||_2 / ||Y_ref||_2 <= 5e-3 and
-    max |Y - Y_ref| <= 2e-2 on outputs of unit scale (the max divided by the
-    outputs' RMS when that exceeds 1).
+    max |Y - Y_ref| <= 2e-2 on outputs of unit scale (fp32 activations of the
+    larger K are scaled by a power of two so that the outputs' RMS is at
+    most 1).
 """
 import numpy as np
 import pytest
 
-from conftest import fixture_names, goldens, load_fixture, normwise_rel
+from conftest import fixture_names, goldens, load_fixture, normwise_rel, unit_scale_act
 
 pytestmark = pytest.mark.gpu
 
@@ -182,6 +183,43 @@ def test_gemv_edge_shapes(q, oracle, wl, gpu):
         q.release(W)
 
 
+@pytest.mark.parametrize("k", [5120, 168 * 128 + 40])
+def test_gemv_nonfinite_activations(q, oracle, wl, gpu, k):
+    """Activations holding +-inf and finite values beyond bf16's range
+    (+-3.4e38, which round to infinity in bf16), in some tokens of a batch:
+    each output is NaN, +inf or -inf exactly where the reference's fmaf
+    chain (qwen35-c/src/q35_mm.c:110-111,135-137) makes it so, and the
+    finite outputs meet the GEMV bar.  K = 5120 runs the row-split GEMV,
+    168 blocks (+40 columns) the stream-K one."""
+    n, m = 700, 5
+    W, sc = wl.gen_weight(0x51E50900 + k, n, k)
+    X = wl.gen_act(0x51E50901 + k, m, k)
+    rng = np.random.default_rng(k)
+    # token 0: one +inf; token 1: +inf and -inf; token 2: two huge finite
+    # values of both signs; token 3: huge values and one -inf; token 4 plain
+    X[0, rng.integers(k)] = np.inf
+    X[1, 7] = np.inf
+    X[1, k - 3] = -np.inf
+    X[2, 100] = np.float32(3.4e38)
+    X[2, k // 2] = np.float32(-3.39e38)
+    X[3, 5] = np.float32(-3.4028235e38)
+    X[3, k - 1] = -np.inf
+    Y = q.mm_fp8_batch(W, sc, X)
+    Yr = oracle.mm_batch(W, sc, X)
+    assert np.array_equal(np.isnan(Y), np.isnan(Yr))
+    assert np.array_equal(np.isposinf(Y), np.isposinf(Yr))
+    assert np.array_equal(np.isneginf(Y), np.isneginf(Yr))
+    assert np.isinf(Yr[0]).any() and np.isnan(Yr[1]).any() and np.isfinite(Yr[2]).all()
+    for t in range(m):
+        fin = np.isfinite(Yr[t])
+        if fin.any():
+            assert normwise_rel(Y[t][fin], Yr[t][fin]) <= GEMV_TOL, t
+    # the plain token is unaffected by its neighbours
+    Y4 = q.mm_fp8_batch(W, sc, np.ascontiguousarray(X[4:5]))
+    assert np.array_equal(Y4[0], Y[4])
+    q.release(W)
+
+
 def test_zero_sizes(q):
     y = q.mm_fp8(np.zeros((4, 0), np.uint8), np.zeros((1, 0), np.uint16), np.zeros(0, np.float32))
     assert (y == 0).all()
@@ -189,14 +227,13 @@ def test_zero_sizes(q):
 
 # ------------------------------------------------------------ prefill GEMM
 def _gemm_check(Y, Yr):
-    """Relative L2 error and max |Y - Y_ref| on outputs of unit scale: the
-    max is divided by the outputs' RMS when that exceeds 1 (K = 17408 with
-    weights ~N(0, 0.02) gives outputs of RMS ~2.6, whose bf16-rounding
-    errors reach 2e-2 in absolute terms at a relative L2 of 1.7e-3)."""
+    """Relative L2 error and max |Y - Y_ref| (absolute: the callers feed
+    activations that keep the outputs' RMS at most 1, unit_scale_act, or
+    bf16-representable ones, whose error is far below the bar)."""
     Y = Y.astype(np.float64)
     Yr = Yr.astype(np.float64)
     rel = np.linalg.norm(Y - Yr) / np.linalg.norm(Yr)
-    mx = np.abs(Y - Yr).max() / max(1.0, float(np.sqrt(np.mean(Yr ** 2))))
+    mx = np.abs(Y - Yr).max()
     return rel, mx
 
 
@@ -248,7 +285,7 @@ def test_gemm_ragged(q, oracle, wl, gpu, m, k, n):
     and 258 x 17408 x 640 slices a second token tile of two rows."""
     import torch
     W, sc = wl.gen_weight(m + k + n, n, k)
-    X = wl.gen_act(m * k, m, k)
+    X = unit_scale_act(wl.gen_act(m * k, m, k), k)
     w = q.Weight(W, sc)
     dX = _torch_dev(X, gpu)
     dY = torch.empty((m, n), dtype=torch.float32, device=gpu)

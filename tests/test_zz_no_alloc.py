@@ -50,6 +50,7 @@ def test_noalloc_equals_matmul(q, oracle, wl, gpu, rows, k, ms):
             Xm = wl.gen_act(rows + 7, m, k)     # same size, other data: nothing carried over
         ya, yb = _both(q, w, _dev(Xm, gpu), m, gpu)
         assert (ya.view(np.uint32) == yb.view(np.uint32)).all(), (rows, k, m)
+        assert q.debug_counters(noalloc=True)[0] == 0   # the shared counters are back at zero
         if m < 64:
             yr = oracle.mm_batch(W, sc, Xm)
             for t in range(m):
@@ -131,5 +132,6 @@ def test_noalloc_in_a_graph(q, wl, gpu):
         assert (Y.cpu().numpy().view(np.uint32) == want.cpu().numpy().view(np.uint32)).all(), r
         q.matmul_noalloc(w, X[:2], other)   # eager use of the same scratch between replays
         torch.cuda.synchronize()
+        assert q.debug_counters(noalloc=True)[0] == 0
     del g
     w.free()
