@@ -192,6 +192,44 @@ void q35mm_release_all(void);
 /* Frees every device resource of the library. */
 void q35mm_shutdown(void);
 
+/* Chained decode GEMVs: a sequence of projections, each reading what
+ * earlier ones wrote (the model's decode calls them one after another,
+ * qwen35-c/src/q35_model.c:877-947), run as ONE persistent launch.  Each
+ * step's weights start streaming before the previous step's outputs are
+ * ready; a step reads its activations only once every earlier step has
+ * completed.  Outputs are bit-identical to calling q35mm_matmul_multi step
+ * by step.
+ *
+ * A step: nw (1..4) weights sharing cols and the device activations x
+ * [m][cols] (the reference's multi4), outputs y[i] [m][rows of w[i]], and
+ * optional residuals resid[i] (y = resid + product; may equal y).  Every
+ * weight must run on the row-split GEMV (cols of 4..160 blocks of 128, as
+ * every projection of the model); m is 1..8 tokens.  x, y and resid may be
+ * outputs of earlier steps.
+ *
+ * q35mm_chain_create uploads the step table once (it allocates);
+ * q35mm_chain_run launches it on a stream and allocates nothing (it may be
+ * captured into a HIP graph); buffers and weights must outlive the chain.
+ * The launch holds every workgroup slot of the device while it runs, and a
+ * step's workgroups wait (bounded) for earlier steps: chain launches on
+ * different streams must not run at the same time -- a wait that gives up
+ * is reported by q35mm_chain_status (which waits for the device).
+ * No counterpart in the reference (its calls return one at a time). */
+typedef struct q35mm_chain q35mm_chain;
+typedef struct q35mm_chain_step {
+    uint32_t nw;
+    const q35mm_weight *w[4];
+    const float *x;
+    float *y[4];
+    const float *resid[4];
+} q35mm_chain_step;
+int q35mm_chain_create(const q35mm_chain_step *steps, uint32_t nsteps, uint32_t m, q35mm_chain **out);
+int q35mm_chain_run(q35mm_chain *chain, void *stream);
+int q35mm_chain_status(q35mm_chain *chain);
+/* Workgroups of one launch (all resident on the device at once). */
+uint32_t q35mm_chain_workgroups(const q35mm_chain *chain);
+void q35mm_chain_destroy(q35mm_chain *chain);
+
 /* Scratch of one stream.  Each stream the device API is called on gets its
  * own scratch set (split partials, counters, staged activations, the MLP
  * block's intermediates: tens to hundreds of MB at prefill sizes), kept

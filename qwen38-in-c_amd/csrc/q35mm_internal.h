@@ -143,6 +143,52 @@ constexpr uint32_t kPairNormMaxCols = 8192;
 __host__ __device__ constexpr uint32_t pair_norm_stride(uint32_t k) { return (((k + 7) / 8 + 3) & ~3u) + 4; }
 hipError_t launch_gemv_pair(const GemvParams &p, bool norm, uint32_t cus, hipStream_t stream);
 
+// ---- chained decode GEMVs (chain.hip) ---------------------------------
+// One step: a row-split GEMV over 1..4 weights sharing x.  seg[i].cta_begin
+// is the first item (32-row sub-tile) of weight i within the step,
+// seg[i].nctas its item count; ws_off, cnt_off and maxc are unused.
+struct ChainStep {
+    GemvSeg seg[4];
+    const float *x;      // [m][ldx] fp32
+    uint32_t ldx, k, kb, nseg;
+    uint32_t items;      // sub-tiles of all segments
+    uint32_t count;      // 1: a later step waits for this one, so its items are counted
+                         // and its ready flags set (the last step's are not)
+    uint32_t wait;       // 1: x or resid are outputs of earlier steps (wait until those have completed)
+    uint32_t x_mode;     // how x and resid are read: kChainX*
+};
+// kChainXPlain: cached loads, allowed when no earlier step of the launch
+// read x's or resid's bytes and at most one wrote them; kChainXCoherent:
+// agent-scope loads at the coherence point.
+constexpr uint32_t kChainXPlain = 0, kChainXCoherent = 2;
+// Counters and flags sit kChainCtrStride bytes apart, each step's ready
+// flags in kChainFlags copies, so that neither atomics nor polls pile onto
+// one cache line.
+constexpr uint32_t kChainFlags = 64;
+constexpr uint32_t kChainCtrStride = 256;
+// Zero floats the activation loads of a block whose inputs are not known
+// to be complete read instead (reloaded once they are).
+constexpr uint32_t kChainZeroFloats = 1024;
+struct ChainParams {
+    const ChainStep *steps;   // device memory, [nsteps]
+    const uint32_t *wg_off;   // [nwg + 1]: workgroup w's items are wg_items[wg_off[w] .. wg_off[w + 1])
+    const uint32_t *wg_items; // (step << 16) | item, in step order
+    const float *zero;        // kChainZeroFloats zeros
+    uint8_t *done;            // step s: uint32 at s * stride, parts finished (zero between launches)
+    uint8_t *ready;           // step s, copy c: uint32 at (s * kChainFlags + c) * stride (zero between launches)
+    uint32_t *exit_cnt;       // workgroups finished, zero between launches
+    uint32_t *err;            // set to 1 when a wait gave up
+    uint32_t nsteps;
+    uint32_t m;
+    uint32_t nwg;             // one workgroup per CU
+    uint32_t spin_limit;      // polls before a wait gives up
+    uint32_t coherent;        // some step's x_mode is kChainXCoherent: every step reads that way
+};
+// Dynamic LDS of a chain launch: the wavefronts' A-operand slots, padded so
+// that one workgroup fills a CU (kChainLds).
+constexpr size_t kChainLds = 96 * 1024;
+hipError_t launch_chain(const ChainParams &p, hipStream_t stream);
+
 // ---- prefill GEMM (bf16 MFMA) ----------------------------------------
 constexpr uint32_t kGemmTile = 256;       // BM = BN = 256 per workgroup
 constexpr uint32_t kGemmThreads = 512;    // 8 wavefronts of 128 x 64

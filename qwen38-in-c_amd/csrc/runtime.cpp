@@ -34,6 +34,11 @@ struct q35mm_st {
     st::Archive a;
 };
 
+struct q35mm_chain {
+    void *mem = nullptr;     // step table, item lists, zeros, counters, flags, error word
+    ChainParams p{};
+};
+
 namespace {
 
 thread_local std::string t_last_error;
@@ -1603,6 +1608,188 @@ Q35MM_API void q35mm_shutdown(void) {
     if (g_dev.stream) (void)hipStreamDestroy(g_dev.stream);
     g_dev.stream = nullptr;
     g_dev.id = -1;
+}
+
+// ---------------------------------------------------------------------
+// Chained decode GEMVs
+// ---------------------------------------------------------------------
+Q35MM_API int q35mm_chain_create(const q35mm_chain_step *steps, uint32_t nsteps, uint32_t m, q35mm_chain **out) {
+    if (!steps || !out || nsteps == 0) return set_error(Q35MM_EINVAL, "q35mm_chain_create: need at least one step");
+    *out = nullptr;
+    if (m == 0 || m > kGemvMaxM) return set_error(Q35MM_EINVAL, "q35mm_chain_create: m=%u (1..%u tokens)", m, kGemvMaxM);
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = ensure_device();
+    if (rc) return rc;
+    std::vector<ChainStep> tab(nsteps);
+    for (uint32_t s = 0; s < nsteps; s++) {
+        const q35mm_chain_step &cs = steps[s];
+        if (cs.nw == 0 || cs.nw > 4 || !cs.x)
+            return set_error(Q35MM_EINVAL, "chain step %u: 1..4 weights and an activation pointer needed", s);
+        ChainStep &t = tab[s];
+        memset(&t, 0, sizeof t);
+        uint32_t item = 0;
+        for (uint32_t i = 0; i < cs.nw; i++) {
+            rc = check_weight(cs.w[i]);
+            if (rc) return rc;
+            const Weight &w = cs.w[i]->w;
+            if (w.cols != cs.w[0]->w.cols)
+                return set_error(Q35MM_EINVAL, "chain step %u: weights differ in cols (%u, %u)", s, cs.w[0]->w.cols,
+                                 w.cols);
+            if (!gemv_rows_shape(w.kb, 4))
+                return set_error(Q35MM_EINVAL, "chain step %u: a %ux%u weight does not run on the row-split GEMV "
+                                 "(K of 4..%u blocks of 128)", s, w.rows, w.cols, kGemvRsMaxKb);
+            if (!cs.y[i]) return set_error(Q35MM_EINVAL, "chain step %u: null output %u", s, i);
+            GemvSeg &g = t.seg[i];
+            g.codes = w.codes;
+            g.scale = w.scale;
+            g.y = cs.y[i];
+            g.resid = cs.resid[i];
+            g.rows = w.rows;
+            g.ldy = w.rows;
+            g.nb = w.nb;
+            g.cta_begin = item;
+            g.nctas = (w.rows + kSubRows - 1) / kSubRows;
+            item += g.nctas;
+        }
+        t.x = cs.x;
+        t.ldx = t.k = cs.w[0]->w.cols;
+        t.kb = cs.w[0]->w.kb;
+        t.nseg = cs.nw;
+        t.items = item;
+        t.wait = s > 0 ? 1u : 0u;
+    }
+    // How each step reads x and resid.  Cached loads are safe where no cache
+    // of the device can hold a line of those bytes from before their
+    // producer's (write-through) stores: no earlier step read them and at
+    // most one wrote them (the launch's start invalidates the caches).  A
+    // step's outputs must not overlap its own activations.
+    struct Span {
+        uintptr_t lo, hi;
+        bool meets(const Span &o) const { return lo < o.hi && o.lo < hi; }
+    };
+    auto span = [&](const void *p, size_t floats) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        return Span{a, a + floats * sizeof(float)};
+    };
+    std::vector<std::vector<Span>> reads(nsteps), writes(nsteps);
+    for (uint32_t s = 0; s < nsteps; s++) {
+        const q35mm_chain_step &cs = steps[s];
+        const uint32_t k = cs.w[0]->w.cols;
+        reads[s].push_back(span(cs.x, (size_t)(m - 1) * k + k));
+        for (uint32_t i = 0; i < cs.nw; i++) {
+            const uint32_t rows = cs.w[i]->w.rows;
+            if (cs.resid[i]) reads[s].push_back(span(cs.resid[i], (size_t)m * rows));
+            writes[s].push_back(span(cs.y[i], (size_t)m * rows));
+            if (writes[s].back().meets(reads[s][0]))
+                return set_error(Q35MM_EINVAL, "chain step %u: output %u overlaps the step's activations", s, i);
+        }
+    }
+    for (uint32_t s = 0; s < nsteps; s++) {
+        bool fresh = true;
+        uint32_t writers = 0;
+        for (uint32_t t = 0; t < s && fresh; t++) {
+            bool w = false;
+            for (const Span &r : reads[s]) {
+                for (const Span &o : reads[t]) fresh &= !r.meets(o);
+                for (const Span &o : writes[t]) w |= r.meets(o);
+            }
+            writers += w;
+        }
+        fresh &= writers <= 1;
+        tab[s].x_mode = fresh ? kChainXPlain : kChainXCoherent;
+        tab[s].count = s + 1 < nsteps ? 1u : 0u;   // every later step waits for all earlier ones
+    }
+    // One workgroup per CU.  Step s's items are dealt round robin over the
+    // workgroups, continuing where step s-1's ended; each workgroup's list is
+    // in step order ((step << 16) | item).
+    const uint32_t G = g_dev.cus;
+    if (nsteps > 0xFFFFu) return set_error(Q35MM_EINVAL, "a chain holds at most 65535 steps");
+    std::vector<std::vector<uint32_t>> lists(G);
+    uint64_t dealt = 0;
+    for (uint32_t s = 0; s < nsteps; s++) {
+        if (tab[s].items > 0xFFFFu) return set_error(Q35MM_EINVAL, "chain step %u: more than 65535 sub-tiles", s);
+        for (uint32_t j = 0; j < tab[s].items; j++) lists[(dealt + j) % G].push_back((s << 16) | j);
+        dealt += tab[s].items;
+    }
+    std::vector<uint32_t> wg_off(G + 1), wg_items;
+    wg_items.reserve(dealt);
+    for (uint32_t w = 0; w < G; w++) {
+        wg_off[w] = (uint32_t)wg_items.size();
+        wg_items.insert(wg_items.end(), lists[w].begin(), lists[w].end());
+    }
+    wg_off[G] = (uint32_t)wg_items.size();
+
+    auto *c = new q35mm_chain();
+    const size_t stride = kChainCtrStride;
+    auto up = [](size_t b) { return (b + 4095) & ~(size_t)4095; };
+    const size_t tab_bytes = up(nsteps * sizeof(ChainStep));
+    const size_t off_bytes = up(wg_off.size() * sizeof(uint32_t));
+    const size_t items_bytes = up(std::max<size_t>(1, wg_items.size()) * sizeof(uint32_t));
+    const size_t zero_bytes = up(kChainZeroFloats * sizeof(float));
+    const size_t ctr_bytes = up((size_t)nsteps * stride);
+    const size_t flag_bytes = (size_t)nsteps * kChainFlags * stride;
+    const size_t head = tab_bytes + off_bytes + items_bytes;
+    const size_t total = head + zero_bytes + ctr_bytes + flag_bytes + 2 * stride;
+    if (hipMalloc(&c->mem, total) != hipSuccess) {
+        c->mem = nullptr;
+        delete c;
+        return set_error(Q35MM_ENOMEM, "hipMalloc(%zu) for a chain failed", total);
+    }
+    uint8_t *base = static_cast<uint8_t *>(c->mem);
+    c->p.steps = reinterpret_cast<const ChainStep *>(base);
+    c->p.wg_off = reinterpret_cast<const uint32_t *>(base + tab_bytes);
+    c->p.wg_items = reinterpret_cast<const uint32_t *>(base + tab_bytes + off_bytes);
+    c->p.zero = reinterpret_cast<const float *>(base + head);
+    c->p.done = base + head + zero_bytes;
+    c->p.ready = c->p.done + ctr_bytes;
+    c->p.exit_cnt = reinterpret_cast<uint32_t *>(c->p.ready + flag_bytes);
+    c->p.err = reinterpret_cast<uint32_t *>(c->p.ready + flag_bytes + stride);
+    c->p.nsteps = nsteps;
+    c->p.m = m;
+    c->p.nwg = G;
+    c->p.spin_limit = env_u32("Q35MM_CHAIN_SPIN_LIMIT", 1u << 20);
+    for (uint32_t s = 0; s < nsteps; s++) c->p.coherent |= tab[s].x_mode == kChainXCoherent;
+    std::vector<uint8_t> hbuf(head, 0);
+    memcpy(hbuf.data(), tab.data(), nsteps * sizeof(ChainStep));
+    memcpy(hbuf.data() + tab_bytes, wg_off.data(), wg_off.size() * sizeof(uint32_t));
+    if (!wg_items.empty()) memcpy(hbuf.data() + tab_bytes + off_bytes, wg_items.data(), wg_items.size() * 4);
+    if (hipMemcpy(base, hbuf.data(), head, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(base + head, 0, total - head) != hipSuccess) {
+        (void)hipFree(c->mem);
+        delete c;
+        return set_error(Q35MM_EHIP, "chain upload failed");
+    }
+    *out = c;
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_chain_run(q35mm_chain *c, void *stream) {
+    if (!c || !c->mem) return set_error(Q35MM_EINVAL, "null chain");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    HIP_TRY(launch_chain(c->p, pick_stream(stream)));
+    return Q35MM_OK;
+}
+
+Q35MM_API int q35mm_chain_status(q35mm_chain *c) {
+    if (!c || !c->mem) return set_error(Q35MM_EINVAL, "null chain");
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    HIP_TRY(hipDeviceSynchronize());
+    uint32_t err = 0;
+    HIP_TRY(hipMemcpy(&err, c->p.err, sizeof err, hipMemcpyDeviceToHost));
+    if (err)
+        return set_error(Q35MM_EHIP, "a chain launch gave up waiting for an earlier step (another chain launch "
+                         "running at the same time can hold the device's workgroup slots)");
+    return Q35MM_OK;
+}
+
+Q35MM_API uint32_t q35mm_chain_workgroups(const q35mm_chain *c) { return c ? c->p.nwg : 0u; }
+
+Q35MM_API void q35mm_chain_destroy(q35mm_chain *c) {
+    if (!c) return;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    (void)hipDeviceSynchronize();
+    if (c->mem) (void)hipFree(c->mem);
+    delete c;
 }
 
 Q35MM_API int q35mm_stream_release(void *stream) {

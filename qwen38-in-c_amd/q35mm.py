@@ -40,6 +40,12 @@ class Q35mmError(RuntimeError):
     pass
 
 
+class ChainStep(C.Structure):
+    """q35mm_chain_step (include/q35mm/q35mm.h)."""
+    _fields_ = [("nw", C.c_uint32), ("w", C.c_void_p * 4), ("x", C.c_void_p), ("y", C.c_void_p * 4),
+                ("resid", C.c_void_p * 4)]
+
+
 def _load(path: str = LIB_PATH) -> C.CDLL:
     if not os.path.exists(path):
         raise Q35mmError(f"libq35mm.so not built at {path}; run __graft_entry__.build() "
@@ -107,6 +113,13 @@ def _load(path: str = LIB_PATH) -> C.CDLL:
     lib.q35mm_last_error.restype = C.c_char_p
     lib.q35mm_resident_count.restype = C.c_size_t
     lib.q35mm_stream_release.argtypes = [vp]
+    lib.q35mm_chain_create.argtypes = [C.POINTER(ChainStep), C.c_uint32, C.c_uint32, C.POINTER(vp)]
+    lib.q35mm_chain_run.argtypes = [vp, vp]
+    lib.q35mm_chain_status.argtypes = [vp]
+    lib.q35mm_chain_workgroups.argtypes = [vp]
+    lib.q35mm_chain_workgroups.restype = C.c_uint32
+    lib.q35mm_chain_destroy.argtypes = [vp]
+    lib.q35mm_chain_destroy.restype = None
     lib.q35mm_debug_counters.argtypes = [vp, C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
     return lib
 
@@ -289,6 +302,57 @@ class Weight:
         if self.handle:
             lib.q35mm_weight_destroy(self.handle)
             self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Chain:
+    """q35mm_chain_*: decode GEMVs run as one persistent launch.  steps is a
+    list of (weights, x, ys) or (weights, x, ys, resids): 1..4 Weights
+    sharing cols, the device activations x [m][cols] and one output (and
+    optional residual, or None) per weight; x may be an output of an earlier
+    step.  The tensors are kept referenced while the chain lives."""
+
+    def __init__(self, steps, m: int = 1):
+        arr = (ChainStep * len(steps))()
+        self._keep = []
+        for i, st in enumerate(steps):
+            ws, x, ys = st[0], st[1], st[2]
+            rs = st[3] if len(st) > 3 and st[3] is not None else [None] * len(ws)
+            if not 1 <= len(ws) <= 4 or len(ys) != len(ws) or len(rs) != len(ws):
+                raise Q35mmError("a chain step holds 1..4 weights, one output (and residual) each")
+            arr[i].nw = len(ws)
+            arr[i].x = _dptr(x)
+            for j, (w, y, r) in enumerate(zip(ws, ys, rs)):
+                arr[i].w[j] = w.handle
+                arr[i].y[j] = _dptr(y)
+                arr[i].resid[j] = _dptr(r) if r is not None else None
+            self._keep.append((ws, x, ys, rs))
+        h = C.c_void_p()
+        _check(lib.q35mm_chain_create(arr, len(steps), m, C.byref(h)), "q35mm_chain_create")
+        self.handle = h
+        self.steps = len(steps)
+
+    @property
+    def workgroups(self) -> int:
+        return int(lib.q35mm_chain_workgroups(self.handle))
+
+    def run(self, stream=None) -> None:
+        _check(lib.q35mm_chain_run(self.handle, _stream(stream)), "q35mm_chain_run")
+
+    def status(self) -> None:
+        """Waits for the device; raises if a launch gave up waiting."""
+        _check(lib.q35mm_chain_status(self.handle), "q35mm_chain_status")
+
+    def free(self) -> None:
+        if self.handle:
+            lib.q35mm_chain_destroy(self.handle)
+            self.handle = None
+            self._keep = []
 
     def __del__(self):
         try:

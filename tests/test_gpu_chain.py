@@ -1,0 +1,199 @@
+"""The chained decode launch (q35mm_chain_*): a sequence of decode GEMVs,
+each reading what earlier ones wrote, run as one persistent launch.
+
+Every output must have the bits of the same projections called one after
+another (q35mm_matmul_multi per step, the row-split GEMV), which the tests
+check bit for bit: one decoder layer's projections (qkv-like, o_proj-like,
+gate and up as one multi-weight step, down with the residual add) at m = 1,
+3 and 8 tokens; three layers in one launch with their activation buffers
+reused from layer to layer (the coherence of re-read buffers along the
+chain); graph replays with eager work in between; launches queued back to
+back (the counters return to zero by themselves).  One output is also
+checked against the oracle (decode bar ||y - y_ref||_inf / ||y_ref||_inf <=
+1e-5), so the chain's bits are the reference's arithmetic.
+"""
+import numpy as np
+import pytest
+
+from conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-5
+# K -> N of one layer whose outputs feed the next projection's input:
+# qkv-like 5120 -> 4096, o_proj 4096 -> 5120, gate and up 5120 -> 17408,
+# down 17408 -> 5120 (the model's shapes but qkv's rows, so they chain)
+LAYER = [("q", 5120, 4096), ("o", 4096, 5120), ("g", 5120, 17408), ("u", 5120, 17408), ("d", 17408, 5120)]
+
+
+def _layer_weights(q, wl, seed):
+    out = {}
+    for i, (name, k, n) in enumerate(LAYER):
+        W, sc = wl.gen_weight(seed + i, n, k)
+        out[name] = (q.Weight(W, sc), W, sc)
+    return out
+
+
+def _bits(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def _layer_steps(L, x, bufs, resid):
+    """q -> o -> (g, u) -> d (+ resid): each step reads the previous output."""
+    return [([L["q"][0]], x, [bufs["q"]]),
+            ([L["o"][0]], bufs["q"], [bufs["o"]]),
+            ([L["g"][0], L["u"][0]], bufs["o"], [bufs["g"], bufs["u"]]),
+            ([L["d"][0]], bufs["g"], [bufs["d"]], [resid])]
+
+
+def _layer_sequential(q, L, x, bufs, resid, m):
+    q.matmul(L["q"][0], x, bufs["q"], m=m)
+    q.matmul(L["o"][0], bufs["q"], bufs["o"], m=m)
+    q.matmul_multi([L["g"][0], L["u"][0]], bufs["o"], [bufs["g"], bufs["u"]], m=m)
+    # down with the residual: the library's GEMV adds it in its epilogue
+    # only inside the MLP block; the separate call is product then add,
+    # the same single rounding as the epilogue's resid + sum
+    q.matmul(L["d"][0], bufs["g"], bufs["d"], m=m)
+    bufs["d"] += resid
+
+
+def _bufs(torch, gpu, m):
+    return {name: torch.empty((m, n), dtype=torch.float32, device=gpu) for name, _, n in LAYER}
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_chain_layer_equals_sequential_calls(q, oracle, wl, gpu, m):
+    import torch
+    L = _layer_weights(q, wl, 0xC4A1 + m)
+    x = torch.from_numpy(wl.gen_act(0xC4B0 + m, m, 5120)).to(gpu)
+    resid = torch.from_numpy(wl.gen_act(0xC4C0 + m, m, 5120)).to(gpu)
+    want = _bufs(torch, gpu, m)
+    _layer_sequential(q, L, x, want, resid, m)
+    got = _bufs(torch, gpu, m)
+    for b in got.values():
+        b.fill_(float("nan"))
+    ch = q.Chain(_layer_steps(L, x, got, resid), m=m)
+    assert ch.workgroups >= 256
+    ch.run()
+    ch.status()
+    for name in want:
+        assert (_bits(got[name]) == _bits(want[name])).all(), name
+    # the first step against the oracle
+    yq = oracle.mm_batch(L["q"][1], L["q"][2], x.cpu().numpy())
+    for t in range(m):
+        assert normwise_rel(got["q"].cpu().numpy()[t], yq[t]) <= GEMV_TOL
+    ch.free()
+    for w, _, _ in L.values():
+        w.free()
+
+
+def _three_layer_plan(Ls, x0, xa, xb, bufs, resid):
+    """Layer i reads ins[i] and its down step writes outs[i] (xa is written
+    by layer 0, read by layer 1 and written again by layer 2); every layer
+    writes the same q, o, g, u buffers, each re-read by the next step."""
+    ins, outs = [x0, xa, xb], [xa, xb, xa]
+    steps = []
+    for i, L in enumerate(Ls):
+        steps += [([L["q"][0]], ins[i], [bufs["q"]]),
+                  ([L["o"][0]], bufs["q"], [bufs["o"]]),
+                  ([L["g"][0], L["u"][0]], bufs["o"], [bufs["g"], bufs["u"]]),
+                  ([L["d"][0]], bufs["g"], [outs[i]], [resid])]
+    return steps
+
+
+def test_chain_three_layers_reused_buffers(q, wl, gpu):
+    """Three layers in one launch, their buffers reused from layer to layer
+    (each re-read after it was written again): re-read activations must come
+    from the coherence point, not from a cache line that held the earlier
+    layer's values.  The launch is queued twice back to back (the first's
+    last workgroup resets the counters); both give the sequential bits."""
+    import torch
+    m = 1
+    Ls = [_layer_weights(q, wl, 0xC500 + 16 * i) for i in range(3)]
+    x0 = torch.from_numpy(wl.gen_act(0xC5F0, m, 5120) * np.float32(1e-3)).to(gpu)
+    resid = torch.from_numpy(wl.gen_act(0xC5F1, m, 5120)).to(gpu)
+
+    def buffers():
+        b = _bufs(torch, gpu, m)
+        return b, torch.empty((m, 5120), device=gpu), torch.empty((m, 5120), device=gpu)
+    wb, wxa, wxb = buffers()
+    for ws, x, ys, *rs in _three_layer_plan(Ls, x0, wxa, wxb, wb, resid):
+        if len(ws) == 1:
+            q.matmul(ws[0], x, ys[0], m=m)
+        else:
+            q.matmul_multi(ws, x, ys, m=m)
+        if rs:
+            ys[0] += rs[0][0]
+    torch.cuda.synchronize()
+    gb, gxa, gxb = buffers()
+    ch = q.Chain(_three_layer_plan(Ls, x0, gxa, gxb, gb, resid), m=m)
+    for rep in range(2):
+        for t in list(gb.values()) + [gxa, gxb]:
+            t.fill_(float("nan"))
+        ch.run()
+        ch.run()
+        ch.status()
+        for name in ("q", "o", "g", "u"):
+            assert (_bits(gb[name]) == _bits(wb[name])).all(), (rep, name)
+        assert (_bits(gxa) == _bits(wxa)).all() and (_bits(gxb) == _bits(wxb)).all(), rep
+    ch.free()
+    for L in Ls:
+        for w, _, _ in L.values():
+            w.free()
+
+
+def test_chain_in_a_graph(q, wl, gpu):
+    """A chain launch captured into a HIP graph: replays with eager library
+    calls in between give the eager bits (no counter clearing is recorded:
+    the kernel resets its counters itself)."""
+    import torch
+    m = 2
+    L = _layer_weights(q, wl, 0xC600)
+    x = torch.from_numpy(wl.gen_act(0xC610, m, 5120)).to(gpu)
+    resid = torch.from_numpy(wl.gen_act(0xC611, m, 5120)).to(gpu)
+    want = _bufs(torch, gpu, m)
+    _layer_sequential(q, L, x, want, resid, m)
+    got = _bufs(torch, gpu, m)
+    ch = q.Chain(_layer_steps(L, x, got, resid), m=m)
+    ch.run()                                   # warm
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ch.run()
+    torch.cuda.synchronize()
+    other = torch.empty((m, 4096), device=gpu)
+    for r in range(3):
+        for b in got.values():
+            b.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for name in want:
+            assert (_bits(got[name]) == _bits(want[name])).all(), (r, name)
+        q.matmul(L["q"][0], x, other, m=m)     # eager work between replays
+        torch.cuda.synchronize()
+    ch.status()
+    del g
+    ch.free()
+    for w, _, _ in L.values():
+        w.free()
+
+
+def test_chain_refuses_other_shapes(q, wl, gpu):
+    """Weights beyond the row-split GEMV's K range (here 168 blocks) and
+    m outside 1..8 are refused with an error, nothing launched."""
+    import torch
+    W, sc = wl.gen_weight(0xC700, 256, 168 * 128)
+    w = q.Weight(W, sc)
+    x = torch.zeros((1, 168 * 128), device=gpu)
+    y = torch.empty((1, 256), device=gpu)
+    with pytest.raises(q.Q35mmError, match="row-split"):
+        q.Chain([([w], x, [y])], m=1)
+    W2, sc2 = wl.gen_weight(0xC701, 256, 1024)
+    w2 = q.Weight(W2, sc2)
+    with pytest.raises(q.Q35mmError, match="m=9"):
+        q.Chain([([w2], torch.zeros((9, 1024), device=gpu), [torch.empty((9, 256), device=gpu)])], m=9)
+    w.free()
+    w2.free()
