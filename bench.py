@@ -162,6 +162,7 @@ def host_cpu_info() -> dict:
 
 
 CPU_CHILD = "--cpu-child"
+SINGLE_COPIES = 41   # configuration 0: distinct 26 MB weight copies, 1.07 GB (GPU and CPU alike)
 
 
 def cpu_child(budget_s: float) -> None:
@@ -213,14 +214,23 @@ def cpu_child(budget_s: float) -> None:
     t, cnt = med_time(layer, budget_s)
     out["layer"] = {"GBps": round(lb / t / 1e9, 3), "ms": round(t * 1e3, 3), "passes": cnt, "bytes": lb}
     del base
-    # configuration 0: one 5120 x 5120 GEMV
+    # configuration 0: one 5120 x 5120 GEMV, each call on the next of 41
+    # distinct copies (1.07 GB, as on the GPU): one 26 MB weight called over
+    # and over would be served by the host's last-level cache, not DRAM
     _, k, n = wl.SINGLE_SHAPE
     W, sc = wl.gen_weight(wl.SEED_BASE + 0, n, k)
     x = wl.gen_act(wl.SEED_BASE + 0x100, 1, k)[0]
-    t, cnt = med_time(lambda: impl.mm(W, sc, x), budget_s / 4)
+    copies = [W] + [np.ascontiguousarray(W ^ row_sign_mask(n, v)) for v in range(1, SINGLE_COPIES)]
+    turn = [0]
+
+    def single_call():
+        impl.mm(copies[turn[0] % len(copies)], sc, x)
+        turn[0] += 1
+    t, cnt = med_time(single_call, budget_s / 4, at_least=2 * len(copies))
     b0 = wl.algorithmic_bytes(1, k, n)
-    out["single"] = {"GBps": round(b0 / t / 1e9, 3), "ms": round(t * 1e3, 3), "passes": cnt}
-    del W
+    out["single"] = {"GBps": round(b0 / t / 1e9, 3), "ms": round(t * 1e3, 3), "passes": cnt,
+                     "copies": len(copies), "pool_MB": round(len(copies) * W.nbytes / 1e6, 1)}
+    del W, copies
     # the prefill GEMM shapes on a sample of the 512 tokens (bf16-representable)
     mt = 64
     pre = {"tokens": mt}
@@ -509,6 +519,8 @@ def main():
                     help="skip configuration 0 (one 5120 x 5120 GEMV over a >= 1 GB pool of copies)")
     ap.add_argument("--no-model-token", dest="model_token", action="store_false",
                     help="skip the reference model's decode token (288 calls in its order)")
+    ap.add_argument("--no-chain", dest="chain", action="store_false",
+                    help="skip the layer step as one persistent q35mm_chain launch")
     ap.add_argument("--no-host-abi", dest="host_abi", action="store_false",
                     help="skip the per-call time of the drop-in q35_mm_fp8 on host pointers")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
@@ -562,16 +574,24 @@ def main():
         q.matmul_multi([L[GATE], L[UP]], xs[GATE], [ys[GATE], ys[UP]], m=m)
         q.gemv(L[4], xs[4], ys[4], m=m)
 
+    def layer_inputs(x0, Y, m):
+        """What each projection of a layer reads: qkv the layer input x0, every
+        later one an output of the projection before it in the same layer
+        (o_proj the first m*4096 floats of qkv's, gate and up o_proj's, down
+        gate's), so each launch depends on the previous one's result."""
+        k_o = base[1][1]
+        return [x0, Y[0].view(-1)[: m * k_o].view(m, k_o), Y[1], Y[1], Y[GATE]]
+
     def decode_step_fn(m: int, lays, nout: int):
-        xs = [torch.from_numpy(wl.gen_act(100 + i, m, k)).to(dev) for i, (_, k, _, _, _) in enumerate(base)]
-        xs[UP] = xs[GATE]
+        x0 = torch.from_numpy(wl.gen_act(100, m, base[0][1])).to(dev)
         ys = [[torch.empty((m, n), dtype=torch.float32, device=dev) for (_, _, n, _, _) in base]
               for _ in range(nout)]
+        xss = [layer_inputs(x0, Y, m) for Y in ys]
 
         def fn(i):
             li = i % len(lays)
-            layer_call(lays[li], xs, ys[li % nout], m)
-        return fn, xs, ys
+            layer_call(lays[li], xss[li % nout], ys[li % nout], m)
+        return fn, xss[0], ys
 
     step_bytes = {m: sum(wl.algorithmic_bytes(m, k, n) for _, k, n, _, _ in base) for m in (1, 2, 4, 8)}
 
@@ -593,16 +613,49 @@ def main():
     roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("decode_gemv_kernels_m1_layer.md"),
+            "traffic_source": "profile, not this run: profiles/decode_gemv_kernels_m1_layer.md (rocprofv3 --pmc "
+                              "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per launch, factors from a 512 MiB copy)",
             "kernel": ("gemv_fp8_kernel (stream-K)" if rows_split_off else
                        "gemv_rows_kernel (qkv, o_proj, gate+up, down)"), "launches": n_launch,
             "avg_launch_us": round(el / n_launch * 1e6, 3),
             "bytes_per_launch": step_bytes[1] // 4}
     del g
 
+    # ---- the same layer step as ONE persistent launch (q35mm_chain) ----
+    chain_out = None
+    if args.chain:
+        chains = [q.Chain([([L[0]], xs_c[0], [Y[0]]), ([L[1]], xs_c[1], [Y[1]]),
+                           ([L[GATE], L[UP]], xs_c[GATE], [Y[GATE], Y[UP]]), ([L[4]], xs_c[4], [Y[4]])])
+                  for L, Y, xs_c in ((layers[li], ys[li], layer_inputs(xs[0], ys[li], 1))
+                                     for li in range(args.pool))]
+        want = [y.clone() for y in ys[(steps - 1) % args.pool]]
+
+        def chain_step(i):
+            chains[i % args.pool].run()
+        for y in ys[(steps - 1) % args.pool]:
+            y.fill_(float("nan"))
+        el_c, gc = time_graph(torch, chain_step, steps, args.warmup, not args.eager)
+        del gc
+        for c in chains:
+            c.status()
+        for a, b in zip(want, ys[(steps - 1) % args.pool]):
+            assert torch.equal(a, b), "chain launch differs from the four launches"
+        chain_out = {"us_per_layer": round(el_c / steps * 1e6, 2),
+                     "GBps": round(step_bytes[1] * steps / el_c / 1e9, 1),
+                     "frac_of_hbm_peak": round(step_bytes[1] * steps / el_c / 1e9 / HBM_PEAK_GBS, 4),
+                     "launches_per_layer": 1, "workgroups": chains[0].workgroups,
+                     "vs_four_launches": round(el / el_c, 3),
+                     "note": "each layer's four steps (qkv, o_proj, gate+up, down; each reads the previous "
+                             "one's output) as one q35mm_chain launch; outputs bit-identical to the four "
+                             "launches (checked here)"}
+        for c in chains:
+            c.free()
+        log(f"chain: {chain_out}")
+
     # ---- full decode token: the whole stack back to back at M = 1 ----
     stack_out = None
     if args.stack_layers:
-        sfn, _, _ = decode_step_fn(1, stack, 1)
+        sfn, sxs, sys_ = decode_step_fn(1, stack, 1)
         nl = len(stack)
 
         def token(i):
@@ -615,8 +668,25 @@ def main():
                      "ms_per_token": round(el_s / reps * 1e3, 4),
                      "GBps": round(tok_bytes * reps / el_s / 1e9, 1),
                      "frac_of_hbm_peak": round(tok_bytes * reps / el_s / 1e9 / HBM_PEAK_GBS, 4)}
-        log(f"stack: {stack_out}")
         del gs
+        if args.chain:
+            # the whole token as one launch: 4 steps per layer, every layer's
+            # buffers shared (re-read buffers are read at the coherence point)
+            Y = sys_[0]
+            tok = q.Chain([st for L in stack for st in (
+                ([L[0]], sxs[0], [Y[0]]), ([L[1]], sxs[1], [Y[1]]), ([L[GATE], L[UP]], sxs[GATE], [Y[GATE], Y[UP]]),
+                ([L[4]], sxs[4], [Y[4]]))])
+            want = [y.clone() for y in Y]
+            el_t, gt = time_graph(torch, lambda _i: tok.run(), reps, 1, not args.eager)
+            del gt
+            tok.status()
+            for a, b in zip(want, Y):
+                assert torch.equal(a, b), "token chain differs from the launches"
+            tok.free()
+            stack_out["chain_ms_per_token"] = round(el_t / reps * 1e3, 4)
+            stack_out["chain_GBps"] = round(tok_bytes * reps / el_t / 1e9, 1)
+            stack_out["chain_note"] = "the same token as one q35mm_chain launch of 4 x layers steps"
+        log(f"stack: {stack_out}")
 
     # ---- configuration 0: one 5120 x 5120 GEMV over a >= 1 GB pool ----
     single = None
@@ -725,7 +795,7 @@ def main():
     prefill = None
     prefill_short = {}
     if not args.no_prefill:
-        prefill = {}
+        calls = {}
         for i, (name, k, n) in enumerate(wl.PREFILL_SHAPES):
             W, sc = wl.gen_weight(wl.SEED_BASE + 2 + 32 * i, n, k)
             w = q.Weight(W, sc)
@@ -737,8 +807,8 @@ def main():
                 q.gemm(w, X, Y)
             el_p, gp = time_graph(torch, call, args.prefill_reps, 2, not args.eager)
             tf = wl.flops(512, k, n) * args.prefill_reps / el_p / 1e12
-            prefill[name] = {"m": 512, "k": k, "n": n, "TFLOPs": round(tf, 1),
-                             "us": round(el_p / args.prefill_reps * 1e6, 1)}
+            calls[name] = {"m": 512, "k": k, "n": n, "TFLOPs": round(tf, 1),
+                           "us": round(el_p / args.prefill_reps * 1e6, 1)}
             log(f"prefill {name}: {tf:.1f} TFLOP/s")
             del gp
             # short prompts: the first m tokens, on the narrow 128 x 512 tiles
@@ -767,24 +837,42 @@ def main():
                 def call_blas(_i, Wb=Wb, Xb=Xb, Yb=Yb):
                     torch.mm(Xb, Wb.t(), out=Yb)
                 el_b, gb = time_graph(torch, call_blas, args.prefill_reps, 2, not args.eager)
-                prefill[name]["hipblaslt_bf16_TFLOPs"] = round(wl.flops(512, k, n) * args.prefill_reps / el_b / 1e12, 1)
-                log(f"prefill {name}: hipBLASLt bf16 {prefill[name]['hipblaslt_bf16_TFLOPs']} TFLOP/s")
+                calls[name]["hipblaslt_bf16_TFLOPs"] = round(wl.flops(512, k, n) * args.prefill_reps / el_b / 1e12, 1)
+                log(f"prefill {name}: hipBLASLt bf16 {calls[name]['hipblaslt_bf16_TFLOPs']} TFLOP/s")
                 del gb, Wb, Xb, Yb
             del X, Y
             torch.cuda.empty_cache()
         tot_flops = sum(wl.flops(512, k, n) for _, k, n in wl.PREFILL_SHAPES)
-        tot_us = sum(v["us"] for v in prefill.values())
+        tot_us = sum(v["us"] for v in calls.values())
         tf_all = tot_flops / (tot_us * 1e-6) / 1e12
-        prefill["total"] = {"TFLOPs": round(tf_all, 1), "frac_of_bf16_peak": round(tf_all / BF16_PEAK_TFLOPS, 4),
-                            "us": round(tot_us, 1),
-                            "note": "includes the fp32->bf16 activation prepass kernel of each call; "
-                                    "hipblaslt_bf16_TFLOPs = torch.mm of bf16 operands of the same shape "
-                                    "(bf16 output), for context"}
-        prefill["roofline"] = {"bound": "mfma", "achieved": round(tf_all, 1), "peak": BF16_PEAK_TFLOPS,
-                               "unit": "TFLOP/s", "frac": round(tf_all / BF16_PEAK_TFLOPS, 4),
-                               "kernel": "gemm_fp8_kernel (+ act_to_bf16_kernel, gemm_tail_kernel / "
-                                         "gemm_reduce_kernel)",
-                               "flops_per_call": {name: wl.flops(512, k, n) for name, k, n in wl.PREFILL_SHAPES}}
+        # the headline's schema: one step = one gate+up call and one down call
+        prefill = {
+            "metric": "M=512 prefill GEMM TFLOP/s (% MFMA peak)",
+            "value": round(tf_all, 1), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.prefill_reps, "warmup": 2, "ms_per_step": round(tot_us / 1e3, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16 MFMA, fp32 accumulation (fp32 activations rounded to bf16 once per call; "
+                     "e4m3 weights exact in bf16; fp32 block scales)",
+            "data": "synthetic (seeded N(0,0.02) weights quantized per 128x128 block, bf16-representable "
+                    "N(0,1) activations)",
+            "config": {"workload": "prefill GEMM at 512 tokens: 5120->34816 (gate and up of the MLP as one "
+                                   "weight) then 17408->5120 (down); one step = both calls, each from fp32 "
+                                   "activations in HBM to fp32 outputs in HBM",
+                       "m": 512, "shapes": [[k, n] for _, k, n in wl.PREFILL_SHAPES], "launch": (
+                           "hip graph" if not args.eager else "eager")},
+            "roofline": {"bound": "mfma", "achieved": round(tf_all, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf_all / BF16_PEAK_TFLOPS, 4),
+                         "traffic": None,
+                         "kernel": "gemm_fp8_kernel (+ act_to_bf16_kernel, gemm_tail_kernel / "
+                                   "gemm_reduce_kernel): whole calls",
+                         "flops_per_step": tot_flops,
+                         "flops_per_call": {name: wl.flops(512, k, n) for name, k, n in wl.PREFILL_SHAPES}},
+            "cpu_baseline": None,
+            "calls": calls,
+            "note": "value = 2*M*N*K of both calls / the time of both whole calls (the fp32->bf16 activation "
+                    "prepass, the GEMM and its tail or K-slice reduction); hipblaslt_bf16_TFLOPs = torch.mm "
+                    "of bf16 operands of the same shape (bf16 output), for context",
+        }
 
     # ---- BF16 lm_head matvec (q35_mm_bf16): 248320 x 5120 ----
     lm_head = None
@@ -863,12 +951,14 @@ def main():
         "dtype": "e4m3 weights x fp32 activations, fp32 accumulation",
         "data": "synthetic (seeded N(0,0.02) weights quantized per 128x128 block, N(0,1) activations)",
         "config": {"workload": "decode GEMV, M=1, one layer's projections 5120->6144, 4096->5120, "
-                               "5120->17408 x2 (gate+up as one multi4 call), 17408->5120 per step",
+                               "5120->17408 x2 (gate+up as one multi4 call), 17408->5120 per step, "
+                               "each reading the previous projection's output",
                    "m": 1, "pool_layers": args.pool, "bytes_per_step": step_bytes[1],
                    "launch": "hip graph" if not args.eager else "eager"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "decode_sweep": sweep or None,
+        "decode_chain": chain_out,
         "decode_stack": stack_out,
         "single": single,
         "decode_model_token": model_token,
