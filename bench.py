@@ -370,30 +370,119 @@ def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
             "frac_of_hbm_peak": round(tok_bytes * reps / el / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_host_abi(q, wl, calls=200):
+def host_calls_lib():
+    """The C driver of host-pointer call sequences (qwen38-in-c_amd/host_token.c):
+    its call record and q35_host_calls_time, so a sequence of q35_mm_* calls
+    runs from C, as the reference model makes them, with no Python between."""
+    import ctypes as C
+
+    class HostCall(C.Structure):
+        _fields_ = [("kind", C.c_uint32), ("cols", C.c_uint32), ("W", C.c_void_p * 4), ("sc", C.c_void_p * 4),
+                    ("rows", C.c_uint32 * 4), ("x", C.c_void_p), ("y", C.c_void_p * 4)]
+    lib = C.CDLL(os.path.join(ROOT, "qwen38-in-c_amd", "lib", "libq35host_token.so"))
+    lib.q35_host_calls_time.restype = C.c_double
+    lib.q35_host_calls_time.argtypes = [C.POINTER(HostCall), C.c_uint32, C.c_uint32, C.c_uint32]
+    return HostCall, lib
+
+
+def fill_call(c, kind, cols, Ws, scs, x, ys):
+    c.kind, c.cols = kind, cols
+    for i in range(4):
+        has = i < len(Ws) and Ws[i] is not None
+        c.W[i] = Ws[i].ctypes.data if has else None
+        c.sc[i] = scs[i].ctypes.data if has else None
+        c.rows[i] = Ws[i].shape[0] if has else 0
+        c.y[i] = ys[i].ctypes.data if has else None
+    c.x = x.ctypes.data
+
+
+def bench_host_abi(q, wl, calls=1000):
     """Per-call time of the drop-in q35_mm_fp8 (host x in, host y out,
-    synchronous) at configuration 0's and the qkv projection's shape,
-    through ctypes, on an already resident weight."""
+    synchronous) at configuration 0's and the qkv projection's shape, called
+    from C in a loop on an already resident weight."""
     import numpy as np
+    HostCall, lib = host_calls_lib()
     out = {}
     for name, k, n, seed in (("single_5120x5120", 5120, 5120, wl.SEED_BASE + 0),
                              ("qkv_5120x6144", 5120, 6144, wl.SEED_BASE + 1)):
         W, sc = wl.gen_weight(seed, n, k)
         x = wl.gen_act(seed + 0x100, 1, k)[0]
         y = np.empty(n, np.float32)
-        args = (q._p(W, q._u8p), q._p(sc, q._u16p), n, k, q._p(x, q._f32p), q._p(y, q._f32p))
-        fn = q.lib.q35_mm_fp8
-        for _ in range(20):
-            fn(*args)
-        t0 = time.perf_counter()
-        for _ in range(calls):
-            fn(*args)
-        us = (time.perf_counter() - t0) / calls * 1e6
+        lst = (HostCall * 1)()
+        fill_call(lst[0], 0, k, [W], [sc], x, [y])
+        us = lib.q35_host_calls_time(lst, 1, 20, calls)
         out[name] = {"us_per_call": round(us, 2), "calls": calls}
         q.release(W)
-    out["note"] = ("q35_mm_fp8 on host pointers, weight already resident: fingerprint check, x copied in, "
-                   "GEMV, completion flag waited for, y copied out; includes the ctypes call")
+    out["note"] = ("q35_mm_fp8 on host pointers from a C loop (qwen38-in-c_amd/host_token.c), weight already "
+                   "resident: x staged in pinned memory and read there by the GEMV, y written by it into pinned "
+                   "memory, completion flag waited for, fingerprint of the weight checked while the GPU runs")
     return out
+
+
+def bench_host_token(q, wl, layers=64, variants=8, reps=3):
+    """The reference model's decode token through the drop-in ABI: its 288
+    q35_mm_fp8 / q35_mm_fp8_multi4 calls on host pointers in its order
+    (per layer the DeltaNet multi4 and out_proj, or the GQA q, k, v and
+    o_proj, then the MLP's gate+up multi4 and down; qwen35-c/src/q35_model.c:
+    903-937, qwen35-c/src/q35_deltanet.c:325-329,360, qwen35-c/src/q35_attn.c:
+    262,273-275), made from C.  Host weights: `variants` distinct copies of
+    each projection, layer i using copy i % variants (3.9 GB of host weights,
+    resident on the device after the untimed first token; the device streams
+    them from HBM as it would distinct layers, 3.9 GB being far beyond its
+    caches)."""
+    import numpy as np
+    HostCall, lib = host_calls_lib()
+    t0 = time.time()
+
+    def copies(seed, n, k):
+        W, sc = wl.gen_weight(seed, n, k)
+        return [W if v == 0 else (W ^ row_sign_mask(n, v)) for v in range(variants)], sc
+    dn = [copies(wl.SEED_BASE + 0x80 + j, n, k) for j, (_, k, n) in enumerate(wl.MODEL_DELTANET_SHAPES)]
+    gq = [copies(wl.SEED_BASE + 0x90 + j, n, k) for j, (_, k, n) in enumerate(wl.MODEL_GQA_SHAPES)]
+    ml = [copies(wl.SEED_BASE + 0xA0 + j, n, k) for j, (_, k, n) in enumerate(wl.MODEL_MLP_SHAPES)]
+    log(f"host token: {variants} host copies of every projection in {time.time() - t0:.1f}s")
+    xs = {k: wl.gen_act(wl.SEED_BASE + 0xB0 + k, 1, k)[0] for k in (5120, 6144, 17408)}
+    ybuf = {}
+
+    def y_of(n, slot=0):
+        return ybuf.setdefault((n, slot), np.empty(n, np.float32))
+    seq = []
+    idn = igq = 0
+    for li in range(layers):
+        if wl.model_layer_is_gqa(li):
+            v = igq % variants
+            for j in range(3):
+                seq.append((0, 5120, [gq[j][0][v]], [gq[j][1]], xs[5120], [y_of(gq[j][0][v].shape[0])]))
+            seq.append((0, 6144, [gq[3][0][v]], [gq[3][1]], xs[6144], [y_of(5120)]))
+            igq += 1
+        else:
+            v = idn % variants
+            seq.append((1, 5120, [dn[j][0][v] for j in range(4)], [dn[j][1] for j in range(4)], xs[5120],
+                        [y_of(dn[j][0][v].shape[0], j) for j in range(4)]))
+            seq.append((0, 6144, [dn[4][0][v]], [dn[4][1]], xs[6144], [y_of(5120)]))
+            idn += 1
+        v = li % variants
+        seq.append((1, 5120, [ml[0][0][v], ml[1][0][v]], [ml[0][1], ml[1][1]], xs[5120],
+                    [y_of(17408, 0), y_of(17408, 1)]))
+        seq.append((0, 17408, [ml[2][0][v]], [ml[2][1]], xs[17408], [y_of(5120)]))
+    lst = (HostCall * len(seq))()
+    for c, (kind, cols, Ws, scs, x, ys) in zip(lst, seq):
+        fill_call(c, kind, cols, Ws, scs, x, ys)
+    t0 = time.time()
+    us = lib.q35_host_calls_time(lst, len(seq), 1, reps)
+    log(f"host token: {len(seq)} calls, {us / 1e3:.3f} ms per token ({time.time() - t0:.1f}s incl. first-use uploads)")
+    tok_bytes = 0
+    for li in range(layers):
+        shapes = wl.MODEL_GQA_SHAPES if wl.model_layer_is_gqa(li) else wl.MODEL_DELTANET_SHAPES
+        tok_bytes += sum(wl.algorithmic_bytes(1, k, n) for _, k, n in shapes + wl.MODEL_MLP_SHAPES)
+    for pool in dn + gq + ml:
+        for W in pool[0]:
+            q.release(W)
+    return {"calls_per_token": len(seq), "host_weight_copies": variants, "ms_per_token": round(us / 1e3, 4),
+            "GBps": round(tok_bytes / (us * 1e-6) / 1e9, 1), "bytes_per_token": tok_bytes,
+            "note": "the reference's 288 q35_mm_fp8 / q35_mm_fp8_multi4 calls of one decode token on host "
+                    "pointers, in its order, from a C loop (qwen38-in-c_amd/host_token.c); synchronous calls, "
+                    "each x in and y out through pinned memory"}
 
 
 def bench_upload(q, wl, base, reps: int = 3):
@@ -700,12 +789,22 @@ def main():
         model_token = bench_model_token(q, wl, torch, dev, stack, not args.eager)
         log(f"model token: {model_token}")
 
-    # ---- the drop-in ABI on host pointers: per-call time ----
+    # ---- the drop-in ABI on host pointers: per-call time, and the model's
+    # 288-call token ----
     host_abi = None
     if args.host_abi:
         host_abi = bench_host_abi(q, wl)
         if single:
             host_abi["single_5120x5120"]["device_kernel_us"] = single["us"]
+            host_abi["single_5120x5120"]["overhead_us"] = round(host_abi["single_5120x5120"]["us_per_call"]
+                                                                - single["us"], 2)
+        if args.model_token:
+            tok = bench_host_token(q, wl)
+            if model_token:
+                tok["device_api_ms_per_token"] = model_token["ms_per_token"]
+                tok["overhead_us_per_call"] = round((tok["ms_per_token"] - model_token["ms_per_token"]) * 1e3
+                                                    / tok["calls_per_token"], 2)
+            host_abi["model_token"] = tok
         log(f"host abi: {host_abi}")
 
     # ---- MLP block at M = 1: RMSNorm -> gate/up -> SwiGLU -> down -> residual ----

@@ -61,7 +61,21 @@ def build_library(verbose: bool = False) -> str:
     if msgs and verbose:
         print("\n".join(msgs))
     os.replace(tmp, LIB)
+    build_host_token()
     return LIB
+
+
+HOST_TOKEN = os.path.join(LIBDIR, "libq35host_token.so")
+
+
+def build_host_token() -> str:
+    """The benchmark's C driver of host-pointer call sequences
+    (host_token.c), linked to lib/libq35mm.so."""
+    cc = os.environ.get("CC", "gcc")
+    subprocess.run([cc, "-O2", "-std=gnu11", "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}",
+                    "-o", HOST_TOKEN, os.path.join(PKG, "host_token.c"), f"-L{LIBDIR}", "-lq35mm",
+                    "-Wl,-rpath,$ORIGIN"], check=True)
+    return HOST_TOKEN
 
 
 def dump_asm(outdir: str) -> None:

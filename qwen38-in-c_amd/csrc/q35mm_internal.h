@@ -258,8 +258,6 @@ hipError_t launch_repack(const uint8_t *raw, uint32_t rows, uint32_t cols,
                          hipStream_t stream);
 hipError_t launch_dequant_f32(const Weight &w, float *out, hipStream_t stream);
 hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream);
-// dst[i] = src[i] for i < n (either side may be device-visible host memory).
-hipError_t launch_copy_f32(const float *src, float *dst, size_t n, hipStream_t stream);
 // Stores v into *flag (pinned host memory) once everything queued before it
 // on the stream has completed.
 hipError_t launch_done_flag(uint32_t *flag, uint32_t v, hipStream_t stream);

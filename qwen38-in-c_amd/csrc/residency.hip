@@ -137,21 +137,6 @@ hipError_t launch_decode_bf16(const Weight &w, uint16_t *out, hipStream_t stream
 }
 
 // ---------------------------------------------------------------------
-// Copy of n floats, e.g. host-pointer activations from pinned (device-
-// visible) host memory into HBM: for a few KiB one workgroup reading over
-// the bus finishes sooner than a DMA transfer's setup.
-// ---------------------------------------------------------------------
-__global__ __launch_bounds__(256) void copy_f32_kernel(const float *__restrict__ src, float *__restrict__ dst,
-                                                       size_t n) {
-    const size_t stride = (size_t)gridDim.x * 256;
-    const size_t i0 = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
-    const size_t n4 = vec ? n / 4 : 0;
-    for (size_t i = i0; i < n4; i += stride)
-        reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
-    for (size_t i = 4 * n4 + i0; i < n; i += stride) dst[i] = src[i];
-}
-
 // Completion flag of a host-pointer call: runs after the call's kernels on
 // the same stream (so after their completion and end-of-kernel release) and
 // stores v into pinned host memory, where the calling thread waits for it.
@@ -164,13 +149,6 @@ __global__ __launch_bounds__(64) void done_flag_kernel(uint32_t *flag, uint32_t 
 
 hipError_t launch_done_flag(uint32_t *flag, uint32_t v, hipStream_t stream) {
     hipLaunchKernelGGL(done_flag_kernel, dim3(1), dim3(64), 0, stream, flag, v);
-    return hipGetLastError();
-}
-
-hipError_t launch_copy_f32(const float *src, float *dst, size_t n, hipStream_t stream) {
-    if (n == 0) return hipSuccess;
-    const size_t blocks = std::min<size_t>(64, (n + 4095) / 4096);
-    hipLaunchKernelGGL(copy_f32_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, src, dst, n);
     return hipGetLastError();
 }
 

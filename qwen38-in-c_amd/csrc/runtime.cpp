@@ -115,7 +115,7 @@ struct Device {
     hipEvent_t up_ev[4] = {};
     void *pin = nullptr;   // pinned host staging
     size_t pin_cap = 0;
-    uint32_t *done = nullptr;   // pinned completion flag of host-pointer calls
+    uint32_t *done = nullptr;   // pinned completion word of host-pointer calls
     uint32_t done_seq = 0;
     bool done_spin = true;      // Q35MM_HOST_WAIT=sync: hipStreamSynchronize instead
     uint32_t gemm_min_m = 64;
@@ -858,15 +858,25 @@ void drop(Resident &r) {
 }
 
 // Resident copy for host W; uploads on first use or when the buffer behind
-// the pointer changed (shape, scale pointer or fingerprint).
+// the pointer changed (shape, scale pointer or fingerprint).  With hit
+// given, a copy found by pointer with the same shape and scale pointer is
+// returned without reading W (*hit = true): the caller checks the
+// fingerprint with resident_same while the device runs the call, and
+// forgets the copy and repeats the call if it differs.
 int resident_fp8(const uint8_t *W, const uint16_t *sc, uint32_t rows, uint32_t cols,
-                 q35mm_weight **out) {
+                 q35mm_weight **out, bool *hit = nullptr) {
     const size_t wbytes = (size_t)rows * cols;
     const size_t scbytes = (size_t)((rows + 127) / 128) * ((cols + 127) / 128) * 2;
+    if (hit) *hit = false;
     auto it = g_res.find(W);
     if (it != g_res.end()) {
         Resident &r = it->second;
         bool same = !r.bf16 && r.rows == rows && r.cols == cols && r.scale == sc;
+        if (same && hit) {
+            *hit = true;
+            *out = r.w;
+            return Q35MM_OK;
+        }
         if (same && !g_dev.trust_pointers) same = r.fp == fingerprint(W, wbytes, sc, scbytes);
         if (same) {
             *out = r.w;
@@ -890,12 +900,18 @@ int resident_fp8(const uint8_t *W, const uint16_t *sc, uint32_t rows, uint32_t c
     return Q35MM_OK;
 }
 
-int resident_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, uint16_t **out) {
+int resident_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, uint16_t **out, bool *hit = nullptr) {
     const size_t wbytes = (size_t)rows * cols * 2;
+    if (hit) *hit = false;
     auto it = g_res.find(W);
     if (it != g_res.end()) {
         Resident &r = it->second;
         bool same = r.bf16 && r.rows == rows && r.cols == cols;
+        if (same && hit) {
+            *hit = true;
+            *out = r.bf16_dev;
+            return Q35MM_OK;
+        }
         if (same && !g_dev.trust_pointers) same = r.fp == fingerprint(W, wbytes, nullptr, 0);
         if (same) {
             *out = r.bf16_dev;
@@ -923,30 +939,57 @@ int resident_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, uint16_t **ou
     return Q35MM_OK;
 }
 
-// Waits until everything queued on st has completed.  A flag kernel queued
-// last stores a fresh sequence number into pinned host memory and this
-// thread spins on it: launch + hipStreamSynchronize costs ~11.6 us of host
-// round trip on this system, launch + spinning on such a flag ~6 us.  Past
-// kSpinLimit (a long call) or if the flag never comes (a failed kernel),
-// hipStreamSynchronize takes over and reports any error.
-hipError_t wait_stream(hipStream_t st) {
-    constexpr auto kSpinLimit = std::chrono::microseconds(2000);
-    if (!g_dev.done_spin) return hipStreamSynchronize(st);
-    if (!g_dev.done) {
-        hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&g_dev.done), 64, hipHostMallocDefault);
-        if (e != hipSuccess) {
-            g_dev.done = nullptr;
-            g_dev.done_spin = false;
-            return hipStreamSynchronize(st);
-        }
-        __atomic_store_n(g_dev.done, 0u, __ATOMIC_RELEASE);
+// Whether the bytes behind a resident host pointer are still the ones
+// uploaded (fingerprint of the weight and its scales; scbytes 0 for a bf16
+// weight).
+bool resident_same(const void *W, size_t wbytes, const void *sc, size_t scbytes) {
+    if (g_dev.trust_pointers) return true;
+    auto it = g_res.find(W);
+    return it != g_res.end() && it->second.fp == fingerprint(W, wbytes, sc, scbytes);
+}
+
+void forget(const void *W) {
+    auto it = g_res.find(W);
+    if (it == g_res.end()) return;
+    drop(it->second);
+    g_res.erase(it);
+}
+
+// Pinned completion word of the host-pointer calls.  Fine-grained
+// (coherent) host memory: the device's store reaches the host, and no
+// device cache holds it.
+constexpr uint32_t kWordDone = 0;
+constexpr size_t kWordsBytes = 64;
+
+bool host_words() {
+    if (g_dev.done) return true;
+    if (hipHostMalloc(reinterpret_cast<void **>(&g_dev.done), kWordsBytes, hipHostMallocCoherent) != hipSuccess) {
+        g_dev.done = nullptr;
+        return false;
     }
-    const uint32_t v = ++g_dev.done_seq ? g_dev.done_seq : ++g_dev.done_seq;   // never 0
-    hipError_t e = launch_done_flag(g_dev.done, v, st);
-    if (e != hipSuccess) return e;
+    memset(g_dev.done, 0, kWordsBytes);
+    return true;
+}
+
+uint32_t next_seq(uint32_t &seq) { return ++seq ? seq : ++seq; }   // never 0
+
+// Completion of everything queued on st so far: a flag kernel queued last
+// stores a fresh sequence number into the done word and the calling thread
+// spins on it (post_done, then wait_done).  Launch + hipStreamSynchronize
+// costs ~11.6 us of host round trip on this system, launch + spinning on
+// such a flag ~6 us.  Past kSpinLimit (a long call) or if the flag never
+// comes (a failed kernel), hipStreamSynchronize takes over and reports any
+// error.
+hipError_t post_done(hipStream_t st, uint32_t *v) {
+    *v = next_seq(g_dev.done_seq);
+    return launch_done_flag(g_dev.done + kWordDone, *v, st);
+}
+
+hipError_t wait_done(hipStream_t st, uint32_t v) {
+    constexpr auto kSpinLimit = std::chrono::microseconds(2000);
     const auto t0 = std::chrono::steady_clock::now();
     for (uint32_t i = 0;; i++) {
-        if (__atomic_load_n(g_dev.done, __ATOMIC_ACQUIRE) == v) return hipSuccess;
+        if (__atomic_load_n(g_dev.done + kWordDone, __ATOMIC_ACQUIRE) == v) return hipSuccess;
         __builtin_ia32_pause();
         if ((i & 255) == 255 && std::chrono::steady_clock::now() - t0 > kSpinLimit) break;
     }
@@ -958,14 +1001,27 @@ hipError_t wait_stream(hipStream_t st) {
 // Each queued DMA transfer costs ~8 us of latency (measured: H2D + GEMV +
 // D2H + synchronize 32 us against 17 us for the GEMV launch alone), so small
 // transfers skip the DMA engines: activations up to kDirectBytes are staged
-// in pinned memory and copied into HBM by a one-workgroup kernel, and
-// outputs up to kDirectBytes are written by the matmul kernels straight
-// into pinned (device-visible) host memory.
+// in pinned memory, which the matmul kernels read in place, and outputs up
+// to kDirectBytes are written by the matmul kernels straight into pinned
+// (device-visible) host memory.  (Reading the staged activations in place
+// measured 17.6 us per call at 5120 x 5120 against 22.0 us with a copy
+// kernel into HBM first: the copy's launch and PCIe round trip cost more
+// than the device's cached reads of 20 KB of host memory.)
+//
+// Order of a call: the activations are staged and the copy, the matmul and
+// the completion flag queued; then 'verify' checks the weights behind the
+// caller's pointers (their fingerprints) while the device computes.  A
+// verify that fails returns kStale once the device has finished: the caller
+// forgets those weights and repeats the call.  (Queuing the copy before
+// staging the activations, with the copy waiting on a host-written word,
+// measured ~2 us slower per call: the device's polls of host memory cost
+// more than the launch latency they would hide.)
 constexpr size_t kDirectBytes = 256 * 1024;
+constexpr int kStale = -1000;   // internal: a resident weight changed behind its pointer
 
-template <class Run>
+template <class Run, class Verify>
 int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t *yfloats,
-                   uint32_t nseg, Run run) {
+                   uint32_t nseg, Run run, Verify verify) {
     size_t ytotal = 0;
     for (uint32_t s = 0; s < nseg; s++) ytotal += yfloats[s];
     const bool direct_x = xfloats * sizeof(float) <= kDirectBytes;
@@ -976,24 +1032,41 @@ int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t
     const size_t xpad = (xfloats + 63) & ~(size_t)63;
     if (!rc) rc = grow_pinned((xpad + ytotal) * sizeof(float));
     if (rc) return rc;
+    if (g_dev.done_spin && !host_words()) g_dev.done_spin = false;
     float *px = (float *)g_dev.pin;
     float *py = px + xpad;
     hipStream_t st = g_dev.stream;
+    auto fail = [&](int code) {
+        (void)hipStreamSynchronize(st);
+        return code;
+    };
     memcpy(px, X, xfloats * sizeof(float));
-    if (direct_x)
-        HIP_TRY(launch_copy_f32(px, (float *)g_dev.dx.ptr, xfloats, st));
-    else
-        HIP_TRY(hipMemcpyAsync(g_dev.dx.ptr, px, xfloats * sizeof(float), hipMemcpyHostToDevice, st));
+    hipError_t e = hipSuccess;
+    if (!direct_x) {
+        e = hipMemcpyAsync(g_dev.dx.ptr, px, xfloats * sizeof(float), hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "activation copy: %s", hipGetErrorString(e)));
+    }
     float *dys[4];
     size_t off = 0;
     for (uint32_t s = 0; s < nseg; s++) {
         dys[s] = (direct_y ? py : (float *)g_dev.dy.ptr) + off;
         off += yfloats[s];
     }
-    rc = run((const float *)g_dev.dx.ptr, dys);
-    if (rc) return rc;
-    if (!direct_y) HIP_TRY(hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st));
-    HIP_TRY(wait_stream(st));
+    rc = run(direct_x ? (const float *)px : (const float *)g_dev.dx.ptr, dys);
+    if (rc) return fail(rc);
+    if (!direct_y) {
+        e = hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st);
+        if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "output copy: %s", hipGetErrorString(e)));
+    }
+    uint32_t v = 0;
+    if (g_dev.done_spin) {
+        e = post_done(st, &v);
+        if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "completion flag: %s", hipGetErrorString(e)));
+    }
+    const bool same = verify();
+    e = g_dev.done_spin ? wait_done(st, v) : hipStreamSynchronize(st);
+    if (e != hipSuccess) return set_error(Q35MM_EHIP, "host-pointer call: %s", hipGetErrorString(e));
+    if (!same) return kStale;
     off = 0;
     for (uint32_t s = 0; s < nseg; s++) {
         memcpy(Y[s], py + off, yfloats[s] * sizeof(float));
@@ -1087,14 +1160,23 @@ Q35MM_API void q35_mm_fp8_batch(const uint8_t *W, const uint16_t *scale_bf16, ui
     }
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     int rc = ensure_device();
-    q35mm_weight *w = nullptr;
-    if (!rc) rc = resident_fp8(W, scale_bf16, rows, cols, &w);
-    if (!rc) {
+    const size_t wbytes = (size_t)rows * cols, scbytes = (size_t)((rows + 127) / 128) * ((cols + 127) / 128) * 2;
+    // first with the resident copy checked during the call; if the bytes
+    // behind W changed, again on a fresh upload
+    for (int attempt = 0; attempt < 2 && !rc; attempt++) {
+        q35mm_weight *w = nullptr;
+        bool hit = false;
+        rc = resident_fp8(W, scale_bf16, rows, cols, &w, attempt == 0 ? &hit : nullptr);
+        if (rc) break;
         float *ys[1] = {Y};
         size_t yf[1] = {(size_t)n * rows};
-        rc = host_roundtrip(X, (size_t)n * cols, ys, yf, 1, [&](const float *dx, float **dy) {
-            return run_matmul(w, n, dx, dy[0], g_dev.stream);
-        });
+        rc = host_roundtrip(
+            X, (size_t)n * cols, ys, yf, 1,
+            [&](const float *dx, float **dy) { return run_matmul(w, n, dx, dy[0], g_dev.stream); },
+            [&] { return !hit || resident_same(W, wbytes, scale_bf16, scbytes); });
+        if (rc != kStale) break;
+        forget(W);
+        rc = Q35MM_OK;
     }
     if (rc) die("q35_mm_fp8_batch");
 }
@@ -1121,29 +1203,50 @@ Q35MM_API void q35_mm_fp8_multi4(const uint8_t *W[4], const uint16_t *sc[4], uin
     // replacing it would free an earlier segment's copy while the launch
     // still needs it.
     q35mm_weight *ws[4], *tmp[4] = {};
-    for (uint32_t i = 0; i < nseg && !rc; i++) {
-        const uint32_t s = idx[i];
-        bool clash = false;
-        for (uint32_t j = 0; j < i; j++)
-            clash |= W[idx[j]] == W[s] && (rows[idx[j]] != rows[s] || sc[idx[j]] != sc[s]);
-        if (clash) {
-            const std::vector<float> f = widen_scales(sc[s], rows[s], cols);
-            rc = weight_create(W[s], f.data(), rows[s], cols, &tmp[i]);
-            ws[i] = tmp[i];
-        } else {
-            rc = resident_fp8(W[s], sc[s], rows[s], cols, &ws[i]);
+    bool hit[4] = {};
+    // first with the resident copies checked during the call; if the bytes
+    // behind a pointer changed, again on fresh uploads
+    for (int attempt = 0; attempt < 2 && !rc; attempt++) {
+        for (uint32_t i = 0; i < nseg && !rc; i++) {
+            const uint32_t s = idx[i];
+            bool clash = false;
+            for (uint32_t j = 0; j < i; j++)
+                clash |= W[idx[j]] == W[s] && (rows[idx[j]] != rows[s] || sc[idx[j]] != sc[s]);
+            hit[i] = false;
+            if (clash) {
+                if (!tmp[i]) {
+                    const std::vector<float> f = widen_scales(sc[s], rows[s], cols);
+                    rc = weight_create(W[s], f.data(), rows[s], cols, &tmp[i]);
+                }
+                ws[i] = tmp[i];
+            } else {
+                rc = resident_fp8(W[s], sc[s], rows[s], cols, &ws[i], attempt == 0 ? &hit[i] : nullptr);
+            }
         }
-    }
-    if (!rc) {
+        if (rc) break;
         float *ys[4];
         size_t yf[4];
         for (uint32_t i = 0; i < nseg; i++) {
             ys[i] = y[idx[i]];
             yf[i] = rows[idx[i]];
         }
-        rc = host_roundtrip(x, cols, ys, yf, nseg, [&](const float *dx, float **dy) {
-            return run_gemv(ws, nseg, 1, dx, dy, g_dev.stream);
-        });
+        rc = host_roundtrip(
+            x, cols, ys, yf, nseg,
+            [&](const float *dx, float **dy) { return run_gemv(ws, nseg, 1, dx, dy, g_dev.stream); },
+            [&] {
+                bool same = true;
+                for (uint32_t i = 0; i < nseg; i++) {
+                    const uint32_t s = idx[i];
+                    if (hit[i])
+                        same &= resident_same(W[s], (size_t)rows[s] * cols, sc[s],
+                                              (size_t)((rows[s] + 127) / 128) * ((cols + 127) / 128) * 2);
+                }
+                return same;
+            });
+        if (rc != kStale) break;
+        for (uint32_t i = 0; i < nseg; i++)
+            if (hit[i]) forget(W[idx[i]]);
+        rc = Q35MM_OK;
     }
     for (uint32_t i = 0; i < nseg; i++)
         if (tmp[i]) q35mm_weight_destroy(tmp[i]);
@@ -1158,15 +1261,23 @@ Q35MM_API void q35_mm_bf16(const uint16_t *W, uint32_t rows, uint32_t cols, cons
     }
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     int rc = ensure_device();
-    uint16_t *dw = nullptr;
-    if (!rc) rc = resident_bf16(W, rows, cols, &dw);
-    if (!rc) {
+    for (int attempt = 0; attempt < 2 && !rc; attempt++) {
+        uint16_t *dw = nullptr;
+        bool hit = false;
+        rc = resident_bf16(W, rows, cols, &dw, attempt == 0 ? &hit : nullptr);
+        if (rc) break;
         float *ys[1] = {y};
         size_t yf[1] = {rows};
-        rc = host_roundtrip(x, cols, ys, yf, 1, [&](const float *dx, float **dy) -> int {
-            HIP_TRY(launch_bf16_gemv(dw, rows, cols, dx, dy[0], g_dev.stream));
-            return Q35MM_OK;
-        });
+        rc = host_roundtrip(
+            x, cols, ys, yf, 1,
+            [&](const float *dx, float **dy) -> int {
+                HIP_TRY(launch_bf16_gemv(dw, rows, cols, dx, dy[0], g_dev.stream));
+                return Q35MM_OK;
+            },
+            [&] { return !hit || resident_same(W, (size_t)rows * cols * 2, nullptr, 0); });
+        if (rc != kStale) break;
+        forget(W);
+        rc = Q35MM_OK;
     }
     if (rc) die("q35_mm_bf16");
 }
