@@ -293,6 +293,15 @@ def variant_pool(q, wl, seed, n, k, copies):
     return [q.Weight(W if v == 0 else (W ^ row_sign_mask(n, v)), sc) for v in range(copies)]
 
 
+# What one launch of this shape can reach at all: a raw read (no arithmetic)
+# of the same codes in the row-split decomposition, one graph-replayed
+# launch per copy of the weight; a figure of the committed profile, not
+# measured in this run.
+SINGLE_LAUNCH_CEILING = {"us": 6.36, "GBps": 4120.0, "frac_of_hbm_peak": 0.515,
+                         "source": "profiles/ceilings_raw_read_and_mfma_rate.md (read single 5120->5120, "
+                                   "tiles/2, graph)"}
+
+
 def bench_single(q, wl, torch, dev, steps, warmup, use_graph, pool_bytes=1 << 30):
     """Configuration 0: one 5120 x 5120 GEMV at M = 1, calls rotating over
     distinct resident copies totalling at least pool_bytes (more than the 256
@@ -313,7 +322,8 @@ def bench_single(q, wl, torch, dev, steps, warmup, use_graph, pool_bytes=1 << 30
         w.free()
     return {"m": 1, "k": k, "n": n, "copies": copies, "pool_MB": round(copies * n * k / 1e6, 1),
             "calls": steps, "us": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
-            "frac_of_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": b}
+            "frac_of_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": b,
+            "single_launch_ceiling": SINGLE_LAUNCH_CEILING}
 
 
 def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
