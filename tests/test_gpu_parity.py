@@ -417,6 +417,43 @@ def test_registry_detects_reused_pointer(q, oracle, wl, gpu):
     assert q.resident_count() == 0
 
 
+def test_registry_reused_pointers_multi4_and_bf16(q, oracle, wl, gpu):
+    """The fingerprint of a found pointer is checked while the device runs
+    the call; a mismatch repeats the call on a fresh upload.  multi4 with
+    one of two weights replaced in place (the other unchanged), a batch
+    call, and the BF16 matvec: every result is the new contents'."""
+    q.release_all()
+    W1, s1 = wl.gen_weight(94, 300, 1024)
+    W2, s2 = wl.gen_weight(95, 200, 1024)
+    x = wl.gen_act(96, 1, 1024)[0]
+    X = wl.gen_act(97, 5, 1024)
+    for _ in range(2):
+        q.mm_fp8_multi4([W1, W2], [s1, s2], x)
+    N2, n2 = wl.gen_weight(98, 200, 1024)
+    W2[...] = N2
+    s2[...] = n2
+    ya, yb = q.mm_fp8_multi4([W1, W2], [s1, s2], x)[:2]
+    assert normwise_rel(ya, oracle.mm(W1, s1, x)) <= GEMV_TOL
+    assert normwise_rel(yb, oracle.mm(N2, n2, x)) <= GEMV_TOL
+    N1, n1 = wl.gen_weight(99, 300, 1024)
+    W1[...] = N1
+    s1[...] = n1
+    Y = q.mm_fp8_batch(W1, s1, X)
+    Yr = oracle.mm_batch(N1, n1, X)
+    for t in range(5):
+        assert normwise_rel(Y[t], Yr[t]) <= GEMV_TOL
+    assert q.resident_count() == 2
+    B = (wl.gen_act(100, 96, 256) * np.float32(0.05)).view(np.uint32)
+    Wb = (B >> 16).astype(np.uint16)
+    xb = wl.gen_act(101, 1, 256)[0]
+    q.mm_bf16(Wb, xb)
+    Wb[...] = (Wb.astype(np.uint32) ^ 0x8000).astype(np.uint16)   # every sign flipped
+    yb2 = q.mm_bf16(Wb, xb)
+    assert (yb2.view(np.uint32) == oracle.mm_bf16(Wb, xb).view(np.uint32)).all()
+    q.release_all()
+    assert q.resident_count() == 0
+
+
 # ------------------------------------------------------------- BF16 matvec
 # The BF16 matvec keeps the reference's summation order (eight fmaf chains,
 # ordered final sum), so it is compared bit for bit.
