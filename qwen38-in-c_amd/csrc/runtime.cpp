@@ -1772,11 +1772,14 @@ Q35MM_API int q35mm_chain_create(const q35mm_chain_step *steps, uint32_t nsteps,
     // How each step reads x and resid.  Cached loads are safe where no cache
     // of the device can hold a line of those bytes from before their
     // producer's (write-through) stores: no earlier step read them and at
-    // most one wrote them (the launch's start invalidates the caches).  A
-    // step's outputs must not overlap its own activations.
+    // most one wrote them (the launch's start invalidates the caches).  The
+    // test is made on whole 256-byte spans (cache lines are 128 bytes), so
+    // a line shared with other data read earlier counts as read.  A step's
+    // outputs must not overlap its own activations (byte ranges).
     struct Span {
         uintptr_t lo, hi;
         bool meets(const Span &o) const { return lo < o.hi && o.lo < hi; }
+        Span lines() const { return Span{lo & ~uintptr_t(255), (hi + 255) & ~uintptr_t(255)}; }
     };
     auto span = [&](const void *p, size_t floats) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(p);
@@ -1786,12 +1789,14 @@ Q35MM_API int q35mm_chain_create(const q35mm_chain_step *steps, uint32_t nsteps,
     for (uint32_t s = 0; s < nsteps; s++) {
         const q35mm_chain_step &cs = steps[s];
         const uint32_t k = cs.w[0]->w.cols;
-        reads[s].push_back(span(cs.x, (size_t)(m - 1) * k + k));
+        const Span xs = span(cs.x, (size_t)(m - 1) * k + k);
+        reads[s].push_back(xs.lines());
         for (uint32_t i = 0; i < cs.nw; i++) {
             const uint32_t rows = cs.w[i]->w.rows;
-            if (cs.resid[i]) reads[s].push_back(span(cs.resid[i], (size_t)m * rows));
-            writes[s].push_back(span(cs.y[i], (size_t)m * rows));
-            if (writes[s].back().meets(reads[s][0]))
+            if (cs.resid[i]) reads[s].push_back(span(cs.resid[i], (size_t)m * rows).lines());
+            const Span ys = span(cs.y[i], (size_t)m * rows);
+            writes[s].push_back(ys.lines());
+            if (ys.meets(xs))
                 return set_error(Q35MM_EINVAL, "chain step %u: output %u overlaps the step's activations", s, i);
         }
     }
