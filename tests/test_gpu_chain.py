@@ -8,7 +8,8 @@ gate and up as one multi-weight step, down with the residual add) at m = 1,
 3 and 8 tokens; three layers in one launch with their activation buffers
 reused from layer to layer (the coherence of re-read buffers along the
 chain); graph replays with eager work in between; launches queued back to
-back (the counters return to zero by themselves).  One output is also
+back (the counters return to zero by themselves); a residual written back
+in place into the layer input.  One output is also
 checked against the oracle (decode bar ||y - y_ref||_inf / ||y_ref||_inf <=
 1e-5), so the chain's bits are the reference's arithmetic.
 """
@@ -179,6 +180,49 @@ def test_chain_in_a_graph(q, wl, gpu):
     ch.free()
     for w, _, _ in L.values():
         w.free()
+
+
+def test_chain_residual_in_place(q, wl, gpu):
+    """The model's residual stream: the last step writes x + down(...) back
+    into the layer input x, which the first step read (the last step waits
+    for every earlier one, so the first step's reads are done).  Two layers
+    in one launch, the second reading the x the first updated; bits equal
+    to the same calls made one by one."""
+    import torch
+    m = 2
+    Ls = [_layer_weights(q, wl, 0xC800 + 16 * i) for i in range(2)]
+    x0 = torch.from_numpy(wl.gen_act(0xC8F0, m, 5120) * np.float32(0.01)).to(gpu)
+
+    def plan(x, B):
+        steps = []
+        for L in Ls:
+            steps += [([L["q"][0]], x, [B["q"]]),
+                      ([L["o"][0]], B["q"], [B["o"]]),
+                      ([L["g"][0], L["u"][0]], B["o"], [B["g"], B["u"]]),
+                      ([L["d"][0]], B["g"], [x], [x])]
+        return steps
+    xw = x0.clone()
+    Bw = _bufs(torch, gpu, m)
+    for ws, x, ys, *rs in plan(xw, Bw):
+        if len(ws) == 1:
+            q.matmul(ws[0], x, ys[0] if not rs else Bw["d"], m=m)
+        else:
+            q.matmul_multi(ws, x, ys, m=m)
+        if rs:
+            xw += Bw["d"]
+    torch.cuda.synchronize()
+    xg = x0.clone()
+    Bg = _bufs(torch, gpu, m)
+    ch = q.Chain(plan(xg, Bg), m=m)
+    ch.run()
+    ch.status()
+    assert (_bits(xg) == _bits(xw)).all()
+    for name in ("q", "o", "g", "u"):
+        assert (_bits(Bg[name]) == _bits(Bw[name])).all(), name
+    ch.free()
+    for L in Ls:
+        for w, _, _ in L.values():
+            w.free()
 
 
 def test_chain_refuses_other_shapes(q, wl, gpu):
