@@ -690,12 +690,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
 #pragma unroll
             for (uint32_t jn = 0; jn < kTN; jn++)
 #pragma unroll
-                for (uint32_t r = 0; r < 16; r++) {
-                    const uint32_t mrow = mt * Geo::kTM + out_row(i, r);
+                for (uint32_t e = 0; e < 16; e++) {
+                    const uint32_t mrow = mt * Geo::kTM + out_row(i, e);
                     const uint32_t ncol = nt * Geo::kTR + out_col(jn);
                     if (mrow < p.m && ncol < sg.rows) {
                         const size_t o = (size_t)mrow * sg.ldy + ncol;
-                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][r] : acc[i][jn][r],
+                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][e] : acc[i][jn][e],
                                                     sg.y + o);
                     }
                 }

@@ -272,27 +272,27 @@ void gemv_rows_kernel(GemvParams p) {
     }
     __syncthreads();
     if constexpr (PAIR) {
-        // gate and up of row r0 + n, wavefronts added in order as for one
+        // gate and up of row r0 + col, wavefronts added in order as for one
         // weight, then silu(gate) * up (the bits of the separate kernels)
         if (threadIdx.x < kPairRows * M) {
-            const uint32_t t = threadIdx.x / kPairRows, n = threadIdx.x % kPairRows;
-            float g = red[0][t][n], u = red[0][t][n + kPairRows];
+            const uint32_t t = threadIdx.x / kPairRows, col = threadIdx.x % kPairRows;
+            float g = red[0][t][col], u = red[0][t][col + kPairRows];
 #pragma unroll
             for (uint32_t w = 1; w < NW; w++) {
-                g += red[w][t][n];
-                u += red[w][t][n + kPairRows];
+                g += red[w][t][col];
+                u += red[w][t][col + kPairRows];
             }
-            const uint32_t row = r0 + n;
+            const uint32_t row = r0 + col;
             if (row < r1) sg.y[(size_t)t * sg.ldy + row] = swiglu1(g, u);
         }
         return;
     }
     if (threadIdx.x < kSubRows * M) {
-        const uint32_t t = threadIdx.x >> 5, n = threadIdx.x & 31;
-        float sum = red[0][t][n];
+        const uint32_t t = threadIdx.x >> 5, col = threadIdx.x & 31;
+        float sum = red[0][t][col];
 #pragma unroll
-        for (uint32_t w = 1; w < NW; w++) sum += red[w][t][n];
-        const uint32_t row = r0 + n;
+        for (uint32_t w = 1; w < NW; w++) sum += red[w][t][col];
+        const uint32_t row = r0 + col;
         if (row < r1) {
             const size_t o = (size_t)t * sg.ldy + row;
             sg.y[o] = sg.resid ? sg.resid[o] + sum : sum;
