@@ -346,14 +346,17 @@ def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
     ys = {n: torch.empty(1, n, device=dev) for n in {10240, 6144, 48, 5120, 12288, 1024, 17408}}
     ya, yb, yv = torch.empty(1, 48, device=dev), torch.empty(1, 17408, device=dev), torch.empty(1, 1024, device=dev)
 
-    def token(_i):
+    def token(_i, qkv_multi4=False):
         idn = igq = 0
         for li in range(layers):
             if wl.model_layer_is_gqa(li):
                 q_, k_, v_, o_ = (gq[j][igq] for j in range(4))
-                q.gemv(q_, xs[5120], ys[12288], m=1)
-                q.gemv(k_, xs[5120], ys[1024], m=1)
-                q.gemv(v_, xs[5120], yv, m=1)
+                if qkv_multi4:
+                    q.matmul_multi([q_, k_, v_], xs[5120], [ys[12288], ys[1024], yv], m=1)
+                else:
+                    q.gemv(q_, xs[5120], ys[12288], m=1)
+                    q.gemv(k_, xs[5120], ys[1024], m=1)
+                    q.gemv(v_, xs[5120], yv, m=1)
                 q.gemv(o_, xs[6144], ys[5120], m=1)
                 igq += 1
             else:
@@ -366,6 +369,15 @@ def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
             q.gemv(L[4], xs[17408], ys[5120], m=1)
     el, g = time_graph(torch, token, reps, 1, use_graph)
     del g
+    torch.cuda.synchronize()
+    qkv_sep = [t.clone() for t in (ys[12288], ys[1024], yv)]
+    # The GQA layer's q, k and v read the same x: one q35mm_matmul_multi of
+    # three segments instead of three launches (the caller's choice; the
+    # reference's multi4 entry point takes up to four weights on one x)
+    el4, g = time_graph(torch, lambda i: token(i, qkv_multi4=True), reps, 1, use_graph)
+    del g
+    torch.cuda.synchronize()
+    qkv_same = all(torch.equal(a, b) for a, b in zip(qkv_sep, (ys[12288], ys[1024], yv)))
     tok_bytes = 0
     for li in range(layers):
         shapes = wl.MODEL_GQA_SHAPES if wl.model_layer_is_gqa(li) else wl.MODEL_DELTANET_SHAPES
@@ -373,11 +385,17 @@ def bench_model_token(q, wl, torch, dev, stack, use_graph, reps=3, layers=64):
     for pool in dn + gq:
         for w in pool:
             w.free()
-    n_launch = sum(4 if wl.model_layer_is_gqa(i) else 2 for i in range(layers)) + 2 * layers
+    n_gqa = sum(1 for i in range(layers) if wl.model_layer_is_gqa(i))
+    n_launch = 4 * n_gqa + 2 * (layers - n_gqa) + 2 * layers
     return {"layers": layers, "deltanet_layers": n_dn, "gqa_layers": layers - n_dn,
             "launches_per_token": n_launch, "bytes_per_token": tok_bytes,
             "ms_per_token": round(el / reps * 1e3, 4), "GBps": round(tok_bytes * reps / el / 1e9, 1),
-            "frac_of_hbm_peak": round(tok_bytes * reps / el / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac_of_hbm_peak": round(tok_bytes * reps / el / 1e9 / HBM_PEAK_GBS, 4),
+            "gqa_qkv_multi4": {"launches_per_token": n_launch - 2 * n_gqa,
+                               "ms_per_token": round(el4 / reps * 1e3, 4),
+                               "GBps": round(tok_bytes * reps / el4 / 1e9, 1),
+                               "frac_of_hbm_peak": round(tok_bytes * reps / el4 / 1e9 / HBM_PEAK_GBS, 4),
+                               "q_k_v_bitwise_equal_to_separate_calls": qkv_same}}
 
 
 def host_calls_lib():
@@ -456,31 +474,45 @@ def bench_host_token(q, wl, layers=64, variants=8, reps=3):
 
     def y_of(n, slot=0):
         return ybuf.setdefault((n, slot), np.empty(n, np.float32))
-    seq = []
-    idn = igq = 0
-    for li in range(layers):
-        if wl.model_layer_is_gqa(li):
-            v = igq % variants
-            for j in range(3):
-                seq.append((0, 5120, [gq[j][0][v]], [gq[j][1]], xs[5120], [y_of(gq[j][0][v].shape[0])]))
-            seq.append((0, 6144, [gq[3][0][v]], [gq[3][1]], xs[6144], [y_of(5120)]))
-            igq += 1
-        else:
-            v = idn % variants
-            seq.append((1, 5120, [dn[j][0][v] for j in range(4)], [dn[j][1] for j in range(4)], xs[5120],
-                        [y_of(dn[j][0][v].shape[0], j) for j in range(4)]))
-            seq.append((0, 6144, [dn[4][0][v]], [dn[4][1]], xs[6144], [y_of(5120)]))
-            idn += 1
-        v = li % variants
-        seq.append((1, 5120, [ml[0][0][v], ml[1][0][v]], [ml[0][1], ml[1][1]], xs[5120],
-                    [y_of(17408, 0), y_of(17408, 1)]))
-        seq.append((0, 17408, [ml[2][0][v]], [ml[2][1]], xs[17408], [y_of(5120)]))
-    lst = (HostCall * len(seq))()
-    for c, (kind, cols, Ws, scs, x, ys) in zip(lst, seq):
-        fill_call(c, kind, cols, Ws, scs, x, ys)
+
+    # q, k and v get outputs of their own (k and v have the same length)
+    def sequence(qkv_multi4):
+        seq = []
+        idn = igq = 0
+        for li in range(layers):
+            if wl.model_layer_is_gqa(li):
+                v = igq % variants
+                if qkv_multi4:
+                    seq.append((1, 5120, [gq[j][0][v] for j in range(3)], [gq[j][1] for j in range(3)], xs[5120],
+                                [y_of(gq[j][0][v].shape[0], j) for j in range(3)]))
+                else:
+                    for j in range(3):
+                        seq.append((0, 5120, [gq[j][0][v]], [gq[j][1]], xs[5120], [y_of(gq[j][0][v].shape[0], j)]))
+                seq.append((0, 6144, [gq[3][0][v]], [gq[3][1]], xs[6144], [y_of(5120)]))
+                igq += 1
+            else:
+                v = idn % variants
+                seq.append((1, 5120, [dn[j][0][v] for j in range(4)], [dn[j][1] for j in range(4)], xs[5120],
+                            [y_of(dn[j][0][v].shape[0], j) for j in range(4)]))
+                seq.append((0, 6144, [dn[4][0][v]], [dn[4][1]], xs[6144], [y_of(5120)]))
+                idn += 1
+            v = li % variants
+            seq.append((1, 5120, [ml[0][0][v], ml[1][0][v]], [ml[0][1], ml[1][1]], xs[5120],
+                        [y_of(17408, 0), y_of(17408, 1)]))
+            seq.append((0, 17408, [ml[2][0][v]], [ml[2][1]], xs[17408], [y_of(5120)]))
+        lst = (HostCall * len(seq))()
+        for c, (kind, cols, Ws, scs, x, ys) in zip(lst, seq):
+            fill_call(c, kind, cols, Ws, scs, x, ys)
+        return seq, lst
+    seq, lst = sequence(False)
     t0 = time.time()
     us = lib.q35_host_calls_time(lst, len(seq), 1, reps)
     log(f"host token: {len(seq)} calls, {us / 1e3:.3f} ms per token ({time.time() - t0:.1f}s incl. first-use uploads)")
+    qkv_sep = [y_of(gq[j][0][0].shape[0], j).copy() for j in range(3)]
+    seq4, lst4 = sequence(True)
+    us4 = lib.q35_host_calls_time(lst4, len(seq4), 1, reps)
+    qkv_same = all(np.array_equal(a, y_of(gq[j][0][0].shape[0], j)) for j, a in enumerate(qkv_sep))
+    log(f"host token, GQA q/k/v as one multi4 call: {len(seq4)} calls, {us4 / 1e3:.3f} ms per token")
     tok_bytes = 0
     for li in range(layers):
         shapes = wl.MODEL_GQA_SHAPES if wl.model_layer_is_gqa(li) else wl.MODEL_DELTANET_SHAPES
@@ -490,6 +522,9 @@ def bench_host_token(q, wl, layers=64, variants=8, reps=3):
             q.release(W)
     return {"calls_per_token": len(seq), "host_weight_copies": variants, "ms_per_token": round(us / 1e3, 4),
             "GBps": round(tok_bytes / (us * 1e-6) / 1e9, 1), "bytes_per_token": tok_bytes,
+            "gqa_qkv_multi4": {"calls_per_token": len(seq4), "ms_per_token": round(us4 / 1e3, 4),
+                               "GBps": round(tok_bytes / (us4 * 1e-6) / 1e9, 1),
+                               "q_k_v_bitwise_equal_to_separate_calls": qkv_same},
             "note": "the reference's 288 q35_mm_fp8 / q35_mm_fp8_multi4 calls of one decode token on host "
                     "pointers, in its order, from a C loop (qwen38-in-c_amd/host_token.c); synchronous calls, "
                     "each x in and y out through pinned memory"}
