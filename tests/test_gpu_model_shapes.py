@@ -68,6 +68,20 @@ def test_gqa_qkv_real_shapes_in_call_order(q, oracle, wl, gpu):
         q.release(W)
 
 
+def test_gqa_qkv_as_one_multi4_call(q, wl, gpu):
+    """q, k, v folded into one q35_mm_fp8_multi4 call (three segments, the
+    fourth empty: rows 0, as the reference's multi4 allows): every output the
+    bits of its separate q35_mm_fp8 call."""
+    x = wl.gen_act(wl.SEED_BASE + 0x48, 1, 5120)[0]
+    ws = [wl.gen_weight(wl.SEED_BASE + 0x49 + i, n, 5120) for i, n in enumerate((12288, 1024, 1024))]
+    outs = q.mm_fp8_multi4([W for W, _ in ws], [sc for _, sc in ws], x)
+    assert outs[3] is None
+    for (W, sc), y in zip(ws, outs[:3]):
+        assert (q.mm_fp8(W, sc, x).view(np.uint32) == y.view(np.uint32)).all()
+    for W, _ in ws:
+        q.release(W)
+
+
 def test_out_proj_63_tokens_equal_single_calls(q, wl, gpu):
     """The straggler batch on the decode GEMV (63 < 64 tokens): every row
     the bits of the per-token call the reference makes."""
