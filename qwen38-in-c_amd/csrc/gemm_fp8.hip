@@ -497,23 +497,37 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
         for (uint32_t k = 0; k < kStageLoads; k++) issue_piece(st, buf, k);
     };
 
-    // ---- block scales of the tile's two row groups, staged in LDS ----
+    // ---- block scales of the tile's row groups, staged in LDS ----
     // The loop takes them from registers (one K block per lane, refilled
     // every 64 blocks), so no LDS read of a scale sits between its MFMAs and
-    // nothing waits for one there.  0 past the last row group.  Done before
-    // the first copy is issued, so this barrier drains nothing.
+    // nothing waits for one there.  The table is copied global -> LDS like
+    // the stages (4-byte global_load_lds, issued just before the first
+    // stages' copies), so its latency is the copies' and no register waits
+    // for it: loaded into registers first, one round trip at a time behind a
+    // branch, it held back the first copy by a memory round trip or two.
+    // Entries past the slice's K range repeat its last block (never read);
+    // a row group past the weight's last repeats that group's scales (its
+    // rows are never stored).
+    constexpr uint32_t kScPer = 2 * kGemmMaxSliceKb / kGemmThreads;
     float *sc_lds = reinterpret_cast<float *>(lds + kScaleOff);
-    for (uint32_t j = threadIdx.x; j < 2 * kGemmMaxSliceKb; j += kGemmThreads) {
-        const uint32_t g = j / Geo::kSliceKb, kk = j % Geo::kSliceKb;
-        const uint32_t nbg = nt * Geo::kGroups + g;
-        float v = 0.0f;
-        if (nbg < sg.nb && kk < kb1 - kb0) v = sg.scale[(size_t)nbg * KB + kb0 + kk];
-        sc_lds[j] = v;
+    {
+        const uint32_t nkb = kb1 > kb0 ? kb1 - kb0 : 1u;
+#pragma unroll
+        for (uint32_t i = 0; i < kScPer; i++) {
+            const uint32_t j0 = wv * 64 + i * kGemmThreads;   // the wavefront's first entry
+            const uint32_t j = j0 + lane;
+            const uint32_t g = j / Geo::kSliceKb, kk = min(j % Geo::kSliceKb, nkb - 1);
+            const uint32_t nbg = min(nt * Geo::kGroups + g, sg.nb - 1);
+            __builtin_amdgcn_global_load_lds(sg.scale + (size_t)nbg * KB + kb0 + kk, (lds_u8 *)(lds + kScaleOff) + j0 * 4,
+                                             4, 0, 0);
+        }
     }
-    __syncthreads();
+    issue(st0, 0);
+    issue(min(st0 + 1, st1 - 1), 1);
+    issue(min(st0 + 2, st1 - 1), 2);
     const float *my_sc = sc_lds + (wn >> 1) * Geo::kSliceKb - kb0;   // indexed by kb
     uint32_t sc_base = kb0;                                           // lane i holds block sc_base + i
-    float sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
+    float sc_lane = 0.0f;   // read once the table has landed (below)
     auto scale_of = [&](uint32_t kb) {   // kb in [sc_base, sc_base + 64)
         return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), kb - sc_base));
     };
@@ -560,12 +574,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     // the conversion's power-of-two scale: 1.0 (exact) for a live block, 0.0
     // (= 2^-127) for a block whose scale is 0, which then adds at most
     // 2^-127 * 448 * |x| per term (and NaN for a NaN code, as lut[code] * 0
-    // does).  No branches around the MFMAs.
-    issue(st0, 0);
-    issue(min(st0 + 1, st1 - 1), 1);
-    issue(min(st0 + 2, st1 - 1), 2);
+    // does).  No branches around the MFMAs.  (The scale table and the first
+    // three stages were issued above: vmcnt <= 2 * kStageLoads means the
+    // table and stage st0 have landed.)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
     lds_barrier();
+    sc_lane = my_sc[min(sc_base + lane, kb1 - 1)];
     Frags f0, f1;
     uint32_t buf = 0;
     // B first, so the next phase's first B sub-tile can be converted
