@@ -9,7 +9,9 @@ gate and up as one multi-weight step, down with the residual add) at m = 1,
 reused from layer to layer (the coherence of re-read buffers along the
 chain); graph replays with eager work in between; launches queued back to
 back (the counters return to zero by themselves); a residual written back
-in place into the layer input.  One output is also
+in place into the layer input; 40 seeded random step lists over a pool of
+buffers (reads, writes, in-place and cross-buffer residuals in every
+order).  One output is also
 checked against the oracle (decode bar ||y - y_ref||_inf / ||y_ref||_inf <=
 1e-5), so the chain's bits are the reference's arithmetic.
 """
@@ -241,3 +243,70 @@ def test_chain_refuses_other_shapes(q, wl, gpu):
         q.Chain([([w2], torch.zeros((9, 1024), device=gpu), [torch.empty((9, 256), device=gpu)])], m=9)
     w.free()
     w2.free()
+
+
+def _random_chains(count=40, seed=0xC5EED):
+    """Seeded step lists over a pool of P activation buffers [m][D]: each
+    step 1..3 weights (D x D) reading one buffer and writing others (never
+    its own x), each output with no residual, itself (y += product, in
+    place) or another buffer not written by the step (x included)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        D = int(rng.choice([1024, 2048]))
+        m = int(rng.choice([1, 2, 3, 5, 8]))
+        P = int(rng.integers(3, 7))
+        steps = []
+        for _s in range(int(rng.integers(1, 9))):
+            xb = int(rng.integers(0, P))
+            others = [b for b in range(P) if b != xb]
+            nw = int(rng.integers(1, min(3, len(others)) + 1))
+            outs = [int(b) for b in rng.choice(others, size=nw, replace=False)]
+            ws = [int(i) for i in rng.choice(6, size=nw, replace=False)]
+            res = []
+            for o in outs:
+                u = rng.random()
+                res.append(None if u < 0.6 else o if u < 0.8 else int(rng.choice([b for b in range(P) if b not in outs])))
+            steps.append((ws, xb, outs, res))
+        out.append((D, m, P, steps))
+    return out
+
+
+def test_chain_random_step_lists(q, wl, gpu):
+    """Random chains: which buffers each step reads and writes decide
+    whether its activations are loaded cached or at the coherence point
+    (reads and writes of earlier steps, on whole cache lines), and every
+    step waits for all earlier ones (so a buffer read earlier may be
+    overwritten).  After two launches of each chain every buffer has the
+    bits of the same steps called one after another (q35mm_matmul_multi,
+    then the residual added)."""
+    import torch
+    pools = {}
+    for c, (D, m, P, steps) in enumerate(_random_chains()):
+        if D not in pools:
+            pools[D] = [q.Weight(*wl.gen_weight(0xC5000 + D + i, D, D)) for i in range(6)]
+        W = pools[D]
+        init = [torch.from_numpy(wl.gen_act(0xC6000 + 97 * c + b, m, D)).to(gpu) for b in range(P)]
+        want = [t.clone() for t in init]
+        for ws, xb, outs, res in steps:
+            tmp = [torch.empty((m, D), device=gpu) for _ in outs]
+            q.matmul_multi([W[i] for i in ws], want[xb], tmp, m=m)
+            new = [tmp[j] + want[r] if r is not None else tmp[j] for j, r in enumerate(res)]
+            for j, o in enumerate(outs):
+                want[o] = new[j]
+        got = [t.clone() for t in init]
+        ch = q.Chain([([W[i] for i in ws], got[xb], [got[o] for o in outs],
+                       [got[r] if r is not None else None for r in res]) for ws, xb, outs, res in steps], m=m)
+        for rep in range(2):
+            if rep:
+                for g, t in zip(got, init):
+                    g.copy_(t)
+            ch.run()
+            ch.status()
+            torch.cuda.synchronize()
+            for b in range(P):
+                assert (_bits(got[b]) == _bits(want[b])).all(), (c, D, m, steps, rep, b)
+        ch.free()
+    for ws in pools.values():
+        for w in ws:
+            w.free()
