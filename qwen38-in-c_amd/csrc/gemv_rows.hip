@@ -295,7 +295,28 @@ void gemv_rows_kernel(GemvParams p) {
         const uint32_t row = r0 + col;
         if (row < r1) {
             const size_t o = (size_t)t * sg.ldy + row;
-            sg.y[o] = sg.resid ? sg.resid[o] + sum : sum;
+            const float v = sg.resid ? sg.resid[o] + sum : sum;
+            if (p.done_word)
+                __hip_atomic_store(sg.y + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            else
+                sg.y[o] = v;
+        }
+    }
+    // Host-pointer calls: the last workgroup to finish stores the call's
+    // completion word (pinned host memory the calling thread polls), in
+    // place of a flag kernel queued after this one.  The outputs were
+    // stored at system scope (through to memory, no cache keeps them); every
+    // wavefront waits for its stores to complete before the workgroup
+    // counts itself, so when the count completes every output of the launch
+    // has reached memory.  The counter returns to zero.
+    if (p.done_word) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            if (__hip_atomic_fetch_add(p.done_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.nctas - 1) {
+                __hip_atomic_store(p.done_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.done_word, p.done_value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         }
     }
 }

@@ -85,6 +85,12 @@ struct GemvParams {
     uint32_t nctas;      // total workgroups
     uint32_t max_range;  // longest range of any segment, in blocks
     uint32_t x_vec;      // x 16-byte aligned, ldx % 4 == 0, k % 8 == 0: vector staging loads
+    // Row-split launches of host-pointer calls: the launch's last workgroup
+    // stores done_value into *done_word (null: nothing); done_cnt counts
+    // finished workgroups and is zero between launches.
+    uint32_t *done_word;
+    uint32_t *done_cnt;
+    uint32_t done_value;
 };
 
 // A-operand rows of the GEMV's staged activations: token x bf16 part (3m),

@@ -117,6 +117,14 @@ struct Device {
     size_t pin_cap = 0;
     uint32_t *done = nullptr;   // pinned completion word of host-pointer calls
     uint32_t done_seq = 0;
+    uint32_t *done_cnt = nullptr;   // device counter of the in-kernel completion (zero between launches)
+    // A host-pointer call's completion word, for the call's last launch to
+    // store if it is a row-split GEMV (taken: it was attached to one).
+    struct DoneReq {
+        uint32_t *word = nullptr;
+        uint32_t value = 0;
+        bool taken = false;
+    } done_req;
     bool done_spin = true;      // Q35MM_HOST_WAIT=sync: hipStreamSynchronize instead
     uint32_t gemm_min_m = 64;
     bool gemm_narrow = true;    // Q35MM_GEMM_NARROW=0: 256-token tiles for every m
@@ -417,8 +425,14 @@ uint32_t gemv_kind(const Weight &w) {
 
 bool uses_gemv_rows(const Weight &w) { return gemv_kind(w) != kStreamK; }
 
+// Launches of at most this many workgroups signal a host-pointer call's
+// completion themselves (one counter all of them add to at their end);
+// longer ones leave it to the flag kernel, whose cost is small beside them.
+constexpr uint32_t kInKernelDoneMaxCtas = 512;
+
 int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const float *dX,
-                   float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid, Scratch *scr) {
+                   float *const *dY, hipStream_t st, const GemvInput &in, float *const *resid, Scratch *scr,
+                   bool last_launch = false) {
     GemvParams p{};
     const uint32_t cols = w[0]->w.cols, KB = w[0]->w.kb;
     p.x = dX;
@@ -456,7 +470,13 @@ int run_gemv_group(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, cons
             cta += g.nctas;
         }
         p.nctas = cta;
+        if (last_launch && g_dev.done_req.word && cta <= kInKernelDoneMaxCtas) {
+            p.done_word = g_dev.done_req.word;
+            p.done_cnt = g_dev.done_cnt;
+            p.done_value = g_dev.done_req.value;
+        }
         HIP_TRY(launch_gemv_rows(p, g_dev.cus, g_dev.rows_waves, g_dev.rows_depth, st));
+        if (p.done_word) g_dev.done_req.taken = true;
         return Q35MM_OK;
     }
     uint32_t cta = 0, wsoff = 0, cntoff = 0, max_range = 1;
@@ -513,7 +533,9 @@ int run_gemv(const q35mm_weight *const *w, uint32_t nseg, uint32_t m, const floa
                 n++;
             }
             if (!n) continue;
-            int rc = run_gemv_group(wg, n, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr, scr);
+            // the call's last launch: the row-split one of the last token group
+            const bool last = t0 + kGemvMaxM >= m && kind == kRows;
+            int rc = run_gemv_group(wg, n, mg, dX + (size_t)t0 * cols, ys, st, ig, resid ? rs : nullptr, scr, last);
             if (rc) return rc;
         }
     }
@@ -963,6 +985,13 @@ constexpr size_t kWordsBytes = 64;
 
 bool host_words() {
     if (g_dev.done) return true;
+    if (!g_dev.done_cnt) {
+        if (hipMalloc(reinterpret_cast<void **>(&g_dev.done_cnt), 256) != hipSuccess) {
+            g_dev.done_cnt = nullptr;
+            return false;
+        }
+        if (hipMemset(g_dev.done_cnt, 0, 256) != hipSuccess) return false;
+    }
     if (hipHostMalloc(reinterpret_cast<void **>(&g_dev.done), kWordsBytes, hipHostMallocCoherent) != hipSuccess) {
         g_dev.done = nullptr;
         return false;
@@ -1052,14 +1081,25 @@ int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t
         dys[s] = (direct_y ? py : (float *)g_dev.dy.ptr) + off;
         off += yfloats[s];
     }
+    // With outputs written straight into pinned memory, the call's last
+    // launch, if a row-split GEMV, stores the completion word itself (no
+    // flag kernel after it); otherwise the flag kernel is queued last.
+    uint32_t v = 0;
+    if (g_dev.done_spin && direct_y) {
+        v = next_seq(g_dev.done_seq);
+        g_dev.done_req.word = g_dev.done + kWordDone;
+        g_dev.done_req.value = v;
+        g_dev.done_req.taken = false;
+    }
     rc = run(direct_x ? (const float *)px : (const float *)g_dev.dx.ptr, dys);
+    const bool done_taken = g_dev.done_req.taken;
+    g_dev.done_req = Device::DoneReq{};
     if (rc) return fail(rc);
     if (!direct_y) {
         e = hipMemcpyAsync(py, g_dev.dy.ptr, ytotal * sizeof(float), hipMemcpyDeviceToHost, st);
         if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "output copy: %s", hipGetErrorString(e)));
     }
-    uint32_t v = 0;
-    if (g_dev.done_spin) {
+    if (g_dev.done_spin && !done_taken) {
         e = post_done(st, &v);
         if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "completion flag: %s", hipGetErrorString(e)));
     }
@@ -1708,6 +1748,8 @@ Q35MM_API void q35mm_shutdown(void) {
     g_dev.pin_cap = 0;
     if (g_dev.done) (void)hipHostFree(g_dev.done);
     g_dev.done = nullptr;
+    if (g_dev.done_cnt) (void)hipFree(g_dev.done_cnt);
+    g_dev.done_cnt = nullptr;
     for (int i = 0; i < 4; i++) {
         if (g_dev.up_pin[i]) (void)hipHostFree(g_dev.up_pin[i]);
         if (g_dev.up_dev[i]) (void)hipFree(g_dev.up_dev[i]);
