@@ -763,6 +763,18 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const TileAt ta = tile_at<MULTI>(p, tile);
     const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
     if (row0 >= p.m) return;   // padding rows: never stored by the slices
+    const GemmSeg &sg = p.seg[ta.seg];
+    const uint32_t col = ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
+    // The residuals (y may be the residual, updated in place) are loaded
+    // first, all four together with the rows and the column clamped in
+    // bounds: loaded one by one between the stores, each waited for the
+    // store before it (the compiler cannot tell y from the residual).
+    float rv[4] = {};
+    if (sg.resid) {
+        const uint32_t c = min(col, sg.rows - 1);
+#pragma unroll
+        for (uint32_t e = 0; e < 4; e++) rv[e] = sg.resid[(size_t)min(row0 + e, p.m - 1) * sg.ldy + c];
+    }
     const float4 *part = reinterpret_cast<const float4 *>(p.ws) + (size_t)st * S * kTileQuads + fq;
     // Up to eight slices' loads in flight, each behind a uniform test (S is
     // the launch's) rather than clamped to the last slice: a clamped load
@@ -782,15 +794,13 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
                 tot.w += v[b].w;
             }
     }
-    const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t col = ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
     const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
     if (col < sg.rows) {
 #pragma unroll
         for (uint32_t e = 0; e < 4; e++)
             if (row0 + e < p.m) {
                 const size_t o = (size_t)(row0 + e) * sg.ldy + col;
-                sg.y[o] = sg.resid ? sg.resid[o] + tv[e] : tv[e];
+                sg.y[o] = sg.resid ? rv[e] + tv[e] : tv[e];
             }
     }
 }
