@@ -10,6 +10,9 @@
 - The host-pointer residency check: a new tensor behind a reused pointer is
   seen; an in-place edit of a few codes outside the sampled fingerprint is
   not, until q35mm_release(W), or always with Q35MM_VERIFY_WEIGHTS=full.
+- The drop-in entry points called from several host threads at once (the
+  reference is called from one thread; the library serialises calls behind
+  one lock): every result the bits of the same call made alone.
 
 Bars: decode GEMV ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5; prefill GEMM
 rel-L2 <= 5e-3 and max-abs <= 2e-2; bitwise where results must equal
@@ -120,6 +123,54 @@ def test_in_place_edit_needs_release(q, oracle, wl, gpu):
     assert normwise_rel(y_new, oracle.mm(W, sc, x)) <= GEMV_TOL
     assert not (y_new.view(np.uint32) == y0.view(np.uint32)).all()
     q.release(W)
+
+
+def test_host_abi_calls_from_several_threads(q, oracle, wl, gpu):
+    """Four host threads calling the drop-in ABI at once, 25 rounds each
+    (ctypes releases the interpreter lock around every call): q35_mm_fp8;
+    q35_mm_fp8_batch on the GEMV (3 tokens) and on the GEMM (64 tokens);
+    q35_mm_fp8_multi4 passing the weight pointer another thread uses;
+    q35_mm_bf16.  Every result the bits of the same call made alone."""
+    import threading
+    rng = np.random.default_rng(0x7EAD)
+    W1, s1 = wl.gen_weight(wl.SEED_BASE + 0x60, 2048, 5120)
+    W2, s2 = wl.gen_weight(wl.SEED_BASE + 0x61, 1024, 4096)
+    W3, s3 = wl.gen_weight(wl.SEED_BASE + 0x62, 48, 5120)
+    W16 = (rng.standard_normal((1536, 2048)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    x1 = wl.gen_act(wl.SEED_BASE + 0x63, 1, 5120)[0]
+    X3 = wl.gen_act(wl.SEED_BASE + 0x64, 3, 4096)
+    X64 = wl.gen_act(wl.SEED_BASE + 0x65, 64, 5120, bf16=True)
+    x16 = rng.standard_normal(2048).astype(np.float32)
+    jobs = [
+        lambda: [q.mm_fp8(W1, s1, x1)],
+        lambda: [q.mm_fp8_batch(W2, s2, X3)],
+        lambda: q.mm_fp8_multi4([W1, W3], [s1, s3], x1)[:2],
+        lambda: [q.mm_fp8_batch(W1, s1, X64), q.mm_bf16(W16, x16)],
+    ]
+    want = [job() for job in jobs]
+    assert normwise_rel(want[0][0], oracle.mm(W1, s1, x1)) <= GEMV_TOL
+    assert (want[3][1].view(np.uint32) == oracle.mm_bf16(W16, x16).view(np.uint32)).all()
+    errors = []
+
+    def worker(j):
+        try:
+            for it in range(25):
+                for a, b in zip(jobs[j](), want[j]):
+                    if not (a.view(np.uint32) == b.view(np.uint32)).all():
+                        errors.append((j, it))
+                        return
+        except Exception as e:   # reported below, in the main thread
+            errors.append((j, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    for W in (W1, W2, W3, W16):
+        q.release(W)
 
 
 def test_verify_weights_full_sees_in_place_edit():
