@@ -251,12 +251,7 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
                     v[e] = col + e < k ? swiglu1(a[e], b[e]) : 0.0f;
                 else
                     v[e] = a[e];
-                // finite values beyond bf16's range saturate to its largest
-                // finite value instead of rounding to infinity (the
-                // reference's fp32 products of such x stay finite);
-                // infinities and NaN pass unchanged
-                if (__builtin_fabsf(v[e]) < __builtin_inff())
-                    v[e] = __builtin_fminf(__builtin_fmaxf(v[e], -0x1.FEp127f), 0x1.FEp127f);
+                v[e] = bf16_saturate(v[e]);
             }
         }
         u32x2_t w = {f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3])};

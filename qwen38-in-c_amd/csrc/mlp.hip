@@ -102,6 +102,87 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *x, u
     for (uint32_t i = tid; i < n; i += kNormThreads) yr[i] = rmsnorm1(xr[i], inv, w[i]);
 }
 
+// The same RMSNorm written straight into the prefill GEMM's activations:
+// bf16 in the lane-order layout of act_to_bf16_kernel (per 32 rows x 128
+// columns, unit u = 64*jq + 32*h + r of 16 bytes holds row r, columns
+// 32*(jq/2) + 16*h + 8*(jq%2) .. +7), rounded as that kernel rounds --
+// the bits of rmsnorm_kernel followed by act_to_bf16_kernel, without the
+// fp32 rows in between.  One workgroup per row of the padded tile rows;
+// thread t owns the groups of eight columns t and t + kNormThreads, whose
+// squares go to the reference's eight lanes (column 8g + e to lane e) and
+// whose outputs fill one 16-byte unit each.  Rows past m and the columns
+// of a partial last K block are written as zeros.  n % 8 == 0, n <=
+// kNormBf16MaxCols, x rows and w 16-byte aligned (the host checks).
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_bf16_kernel(const float *x, uint32_t ldx,
+                                                                    const float *__restrict__ w, uint32_t m,
+                                                                    uint32_t n, uint32_t kb_total, float eps,
+                                                                    uint8_t *xb) {
+#pragma clang fp contract(off)
+    constexpr uint32_t G = kNormBf16MaxCols / (8 * kNormThreads);   // groups per thread
+    __shared__ __align__(16) float sq[8 * kNormLaneStride];
+    __shared__ float lanes[8];
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const uint32_t ng = n / 8, gp = kb_total * (kBlock / 8);   // groups with data / in the layout
+    uint8_t *const base = xb + (size_t)(row / 32) * kb_total * 8 * kChunkBytes;
+    auto unit = [&](uint32_t g) {
+        const uint32_t c = (g % 16) * 8;   // column within its K block
+        const uint32_t u = ((c >> 5) * 2 + ((c >> 3) & 1)) * 64 + ((c >> 4) & 1) * 32 + row % 32;
+        return reinterpret_cast<u32x4_t *>(base + (size_t)(g / 16) * 8 * kChunkBytes + u * 16);
+    };
+    if (row >= m) {
+#pragma unroll
+        for (uint32_t j = 0; j < G; j++) {
+            const uint32_t g = tid + j * kNormThreads;
+            if (g < gp) *unit(g) = u32x4_t{0u, 0u, 0u, 0u};
+        }
+        return;
+    }
+    const float *xr = x + (size_t)row * ldx;
+    float xv[G][8], wv[G][8];
+#pragma unroll
+    for (uint32_t j = 0; j < G; j++) {
+        const uint32_t g = tid + j * kNormThreads;
+        if (g < ng) {
+            const float4 a = *reinterpret_cast<const float4 *>(xr + 8 * g);
+            const float4 b = *reinterpret_cast<const float4 *>(xr + 8 * g + 4);
+            const float4 c = *reinterpret_cast<const float4 *>(w + 8 * g);
+            const float4 d = *reinterpret_cast<const float4 *>(w + 8 * g + 4);
+            xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
+            xv[j][4] = b.x; xv[j][5] = b.y; xv[j][6] = b.z; xv[j][7] = b.w;
+            wv[j][0] = c.x; wv[j][1] = c.y; wv[j][2] = c.z; wv[j][3] = c.w;
+            wv[j][4] = d.x; wv[j][5] = d.y; wv[j][6] = d.z; wv[j][7] = d.w;
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) xv[j][e] = wv[j][e] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < G; j++) {
+        const uint32_t g = tid + j * kNormThreads;
+        if (g < ng) {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) sq[e * kNormLaneStride + g] = xv[j][e] * xv[j][e];
+        }
+    }
+    __syncthreads();
+    if (tid < 8) lanes[tid] = lane_sum_in_order(sq + tid * kNormLaneStride, ng, 0.0f);
+    __syncthreads();
+    float s = lanes[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) s = s + lanes[j];
+    const float inv = rms_inverse(s, n, eps);
+#pragma unroll
+    for (uint32_t j = 0; j < G; j++) {
+        const uint32_t g = tid + j * kNormThreads;
+        if (g >= gp) continue;
+        float v[8];
+#pragma unroll
+        for (uint32_t e = 0; e < 8; e++) v[e] = g < ng ? bf16_saturate(rmsnorm1(xv[j][e], inv, wv[j][e])) : 0.0f;
+        *unit(g) = u32x4_t{f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]),
+                           f32x2_to_bf16x2_rne(v[4], v[5]), f32x2_to_bf16x2_rne(v[6], v[7])};
+    }
+}
+
 __global__ void swiglu_kernel(const float *g, const float *u, float *y, size_t n) {
 #pragma clang fp contract(off)
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -118,6 +199,21 @@ hipError_t launch_rmsnorm(const float *x, uint32_t ldx, const float *w, float *y
                           uint32_t rows, uint32_t n, float eps, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, stream, x, ldx, w, y, ldy, n, eps);
+    return hipGetLastError();
+}
+
+bool rmsnorm_bf16_fits(const float *x, uint32_t ldx, const float *w, uint32_t n) {
+    return n > 0 && n % 8 == 0 && n <= kNormBf16MaxCols && ldx % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+}
+
+hipError_t launch_rmsnorm_bf16(const float *x, uint32_t ldx, const float *w, uint32_t m, uint32_t n, float eps,
+                               uint32_t rows_pad, uint32_t kb, uint16_t *xb, hipStream_t stream) {
+    if (!rmsnorm_bf16_fits(x, ldx, w, n) || rows_pad % 32 != 0 || rows_pad < m || kb * kBlock < n)
+        return hipErrorInvalidValue;
+    if (rows_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3(rows_pad), dim3(kNormThreads), 0, stream, x, ldx, w, m, n, kb, eps,
+                       reinterpret_cast<uint8_t *>(xb));
     return hipGetLastError();
 }
 

@@ -77,6 +77,15 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float a, float b) {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return bits_f32(b << 16); }
 
+// An activation about to be rounded to bf16 for the prefill GEMM: finite
+// values beyond bf16's range saturate to its largest finite value instead of
+// rounding to infinity (the reference's fp32 products of such x stay
+// finite); infinities and NaN pass unchanged.
+__device__ __forceinline__ float bf16_saturate(float v) {
+    return __builtin_fabsf(v) < __builtin_inff() ? __builtin_fminf(__builtin_fmaxf(v, -0x1.FEp127f), 0x1.FEp127f)
+                                                 : v;
+}
+
 // Exact three-way split of two fp32 values into bf16 parts, packed in pairs:
 // x == p0 + p1 + p2 for every normal x (each residual is exact in fp32 and has
 // at most 16, then 8, significant bits).  Each part is a round-to-nearest-even

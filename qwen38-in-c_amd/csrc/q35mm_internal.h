@@ -297,6 +297,15 @@ hipError_t launch_quantize_bf16(const uint16_t *w, uint32_t rows, uint32_t cols,
 // y = silu(g) * u, residual x += y.
 hipError_t launch_rmsnorm(const float *x, uint32_t ldx, const float *w, float *y, uint32_t ldy,
                           uint32_t rows, uint32_t n, float eps, hipStream_t stream);
+// RMSNorm of rows 0..m-1 of x straight into launch_act_to_bf16's layout
+// (rows_pad rows, a multiple of 32, zeros past m; kb K blocks of 128, zeros
+// past n): the bits of launch_rmsnorm followed by launch_act_to_bf16.  For
+// rmsnorm_bf16_fits: n % 8 == 0, n <= kNormBf16MaxCols, rows of x and w
+// 16-byte aligned.
+constexpr uint32_t kNormBf16MaxCols = 8192;
+bool rmsnorm_bf16_fits(const float *x, uint32_t ldx, const float *w, uint32_t n);
+hipError_t launch_rmsnorm_bf16(const float *x, uint32_t ldx, const float *w, uint32_t m, uint32_t n, float eps,
+                               uint32_t rows_pad, uint32_t kb, uint16_t *xb, hipStream_t stream);
 hipError_t launch_swiglu(const float *g, const float *u, float *y, size_t n, hipStream_t stream);
 hipError_t launch_add_inplace(float *x, const float *y, size_t n, hipStream_t stream);
 

@@ -554,9 +554,16 @@ bool gemm_fits(const Weight &w, uint32_t m) {
 // Weights sharing K (cols) and x, one launch over all their tiles.  Optional:
 // resid[s] (y = resid + product, may alias y) and x2 (the activations are
 // silu(x) * x2, formed while rounding them to bf16).
+// RMSNorm applied to the GEMM's activations as they are rounded to bf16
+// (run_gemm's norm): weight w of the activations' length, epsilon eps.
+struct GemmNorm {
+    const float *w;
+    float eps;
+};
+
 int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const float *dX, float *const *dY,
              hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr,
-             Scratch *scr = nullptr) {
+             Scratch *scr = nullptr, const GemmNorm *norm = nullptr) {
     const Weight &w0 = wt[0]->w;
     Scratch &sc = scr ? *scr : scratch_for(st);
     for (uint32_t s = 0; s < nseg; s++) {
@@ -618,8 +625,10 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
     p.narrow = narrow ? 1u : 0u;
-    HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (tile_m / kSubRows), w0.kb,
-                               xb, st));
+    if (norm)
+        HIP_TRY(launch_rmsnorm_bf16(dX, w0.cols, norm->w, m, w0.cols, norm->eps, pl.mtiles * tile_m, w0.kb, xb, st));
+    else
+        HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (tile_m / kSubRows), w0.kb, xb, st));
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -1594,13 +1603,20 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         HIP_TRY(launch_add_inplace(dX, y, nh, st));
         return Q35MM_OK;
     }
-    // Prefill: RMSNorm kernel; gate and up as one GEMM launch; the down GEMM
-    // forms silu(gate) * up while rounding its activations to bf16 and adds
-    // the residual in its epilogue (the bits of the separate calls).
-    HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
+    // Prefill: gate and up as one GEMM launch, the RMSNorm written straight
+    // into its bf16 activations (a separate RMSNorm kernel and fp32 rows
+    // when the row length or alignment does not suit that kernel); the down
+    // GEMM forms silu(gate) * up while rounding its activations to bf16 and
+    // adds the residual in its epilogue (the bits of the separate calls).
     const q35mm_weight *gu[2] = {gate, up};
     float *gy[2] = {g, u};
-    rc = run_gemm(gu, 2, m, xn, gy, st);
+    if (rmsnorm_bf16_fits(dX, H, dNormW, H)) {
+        const GemmNorm nm{dNormW, eps};
+        rc = run_gemm(gu, 2, m, dX, gy, st, nullptr, nullptr, nullptr, &nm);
+    } else {
+        HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
+        rc = run_gemm(gu, 2, m, xn, gy, st);
+    }
     if (rc) return rc;
     const q35mm_weight *dn[1] = {down};
     float *dy[1] = {dX};
