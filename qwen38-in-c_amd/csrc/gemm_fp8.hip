@@ -281,20 +281,52 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const float *__restric
 // K slices of whole 256x256 tiles this writes and re-reads no partial tiles
 // (64 MB for the 16 leftover tiles of a 512 x 34816 x 5120 product) and
 // needs no reduction kernel.
+// Activation t, column c of the lane-order bf16 layout act_to_bf16_kernel
+// writes (per 32 tokens x 128 columns 8 KiB; unit 64*jq + 32*h + t%32 of
+// 16 bytes holds columns 32*(jq/2) + 16*h + 8*(jq%2) .. +7), rounded as that
+// kernel rounds.
+__device__ __forceinline__ void store_act_bf16(uint16_t *act, uint32_t act_kb, uint32_t t, uint32_t c, float v) {
+    const uint32_t cc = c % kBlock;
+    const uint32_t u = ((cc >> 5) * 2 + ((cc >> 3) & 1)) * 64 + ((cc >> 4) & 1) * 32 + t % 32;
+    act[((size_t)(t / 32) * act_kb + c / kBlock) * (4 * kChunkBytes) + u * 8 + (cc & 7)] =
+        (uint16_t)(f32x2_to_bf16x2_rne(v, 0.0f) & 0xFFFFu);
+}
+
+// silu(g) * u of a paired tile, as act_to_bf16_kernel<true> forms it before
+// rounding.
+__device__ __forceinline__ float paired_swiglu(float g, float u) { return bf16_saturate(swiglu1(g, u)); }
+
 constexpr uint32_t kTailTile = 64;
 constexpr uint32_t kTailPerTile = (kGemmTile / kTailTile) * (kGemmTile / kTailTile);   // 16
 constexpr uint32_t kTailDepth = 4;                                                      // chunks in flight
 constexpr uint32_t kTailLds = (kGemmThreads / 64) * kTailTile * kTailTile * 4;          // 128 KiB
 static_assert(kTailLds <= 160 * 1024, "LDS");
 
-template <bool MULTI>
+// PM (paired segments, GemmParams::pair): 0 -- no pairing; 1 -- the small
+// tile holds 32 rows of segment 0 and the same 32 rows of segment 1, fp32
+// outputs; 2 -- the same, writing silu(segment 0) * segment 1 as bf16
+// activations.
+template <bool MULTI, uint32_t PM>
 __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uint8_t *lds) {
+    static_assert(!(MULTI && PM), "paired tiles come from two segments of one shape");
     const uint32_t tile = p.tail_tile0 + idx / kTailPerTile, st = idx % kTailPerTile;
     const TileAt ta = tile_at<MULTI>(p, tile);
     const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t row0 = ta.mt * kGemmTile + (st & 3) * kTailTile;    // token rows
-    const uint32_t col0 = ta.nt * kGemmTile + (st >> 2) * kTailTile;   // weight rows
-    if (row0 >= p.m || col0 >= sg.nb * kBlock) return;                 // the whole workgroup: no work
+    const uint32_t row0 = ta.mt * kGemmTile + (st & 3) * kTailTile;   // token rows
+    // weight rows: 64 of one weight, or (paired) 32 of each segment
+    const uint32_t col0 = PM ? ta.nt * (kGemmTile / 2) + (st >> 2) * (kTailTile / 2)
+                             : ta.nt * kGemmTile + (st >> 2) * kTailTile;
+    if (col0 >= sg.nb * kBlock) return;   // the whole workgroup: no work
+    if (row0 >= p.m) {
+        if constexpr (PM == 2) {   // padding tokens of the activation layout: zeros
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t q = threadIdx.x * 4 + k;   // 64 tokens x 32 columns
+                store_act_bf16(p.act_out, p.act_kb, row0 + q / 32, col0 + q % 32, 0.0f);
+            }
+        }
+        return;
+    }
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -304,8 +336,17 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
     const uint32_t g = col0 / kBlock, s0 = (col0 % kBlock) / kSubRows; // weight group, first sub-tile
     const uint32_t m32 = row0 / kSubRows;
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(p.xb) + lane * 16;
-    const uint8_t *wb = sg.codes + (size_t)g * KB * kBlockBytes + s0 * kSubBytes + lane * 16;
-    const float *sc_g = sg.scale + (size_t)g * KB;
+    // B of MFMA column tile ni: sub-tile s0 + ni of the weight, or (paired)
+    // sub-tile s0 of segment ni; one scale track per weight read.
+    constexpr uint32_t NS = PM ? 2 : 1;
+    const uint8_t *wb[NS];
+    const float *sc_g[NS];
+#pragma unroll
+    for (uint32_t z = 0; z < NS; z++) {
+        const GemmSeg &bs = PM ? p.seg[z] : sg;
+        wb[z] = bs.codes + (size_t)g * KB * kBlockBytes + s0 * kSubBytes + lane * 16;
+        sc_g[z] = bs.scale + (size_t)g * KB;
+    }
 
     // Chunk c = 4 * (kb - k0) + j (32 columns): A for the two 32-row token
     // sub-tiles and both MFMA halves, B (16 e4m3 codes per lane) for the
@@ -324,19 +365,23 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
                     xa + ((size_t)((m32 + mi) * KB + kb) * 8 + j * 2 + q) * kChunkBytes);
 #pragma unroll
         for (uint32_t ni = 0; ni < 2; ni++)
-            ch.b[ni] = *reinterpret_cast<const u32x4_t *>(wb + (size_t)kb * kBlockBytes + ni * kSubBytes +
-                                                           j * kChunkBytes);
+            ch.b[ni] = *reinterpret_cast<const u32x4_t *>(wb[PM ? ni : 0] + (size_t)kb * kBlockBytes +
+                                                           (PM ? 0 : ni) * kSubBytes + j * kChunkBytes);
     };
 
     f32x16_t acc[2][2] = {};
-    float s_prev = 0.0f;   // units of the accumulator (0: nothing live yet)
+    float s_prev[NS] = {};   // units of the accumulators (0: nothing live yet)
     if (k1 > k0) {
         const uint32_t nc = (k1 - k0) * 4;
         Chunk ring[kTailDepth];
 #pragma unroll
         for (uint32_t d = 0; d + 1 < kTailDepth; d++) load(ring[d], min(d, nc - 1));
-        float keep = 1.0f;
-        float sc_next = sc_g[k0];
+        float keep[NS], sc_next[NS];
+#pragma unroll
+        for (uint32_t z = 0; z < NS; z++) {
+            keep[z] = 1.0f;
+            sc_next[z] = sc_g[z][k0];
+        }
         for (uint32_t c0 = 0; c0 < nc; c0 += kTailDepth) {
 #pragma unroll
             for (uint32_t d = 0; d < kTailDepth; d++) {
@@ -349,16 +394,20 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
                         // (block scale 0: the conversion scale 0 acts as
                         // 2^-127, as in the main kernel)
                         const uint32_t kb = k0 + c / 4;
-                        const float sc = sc_next;
-                        sc_next = sc_g[min(kb + 1, k1 - 1)];
-                        const bool live = sc != 0.0f;
-                        keep = live ? 1.0f : 0.0f;
-                        const float r = live ? (s_prev != 0.0f ? s_prev / sc : 0.0f) : 1.0f;
 #pragma unroll
-                        for (uint32_t mi = 0; mi < 2; mi++)
+                        for (uint32_t z = 0; z < NS; z++) {
+                            const float sc = sc_next[z];
+                            sc_next[z] = sc_g[z][min(kb + 1, k1 - 1)];
+                            const bool live = sc != 0.0f;
+                            keep[z] = live ? 1.0f : 0.0f;
+                            const float r = live ? (s_prev[z] != 0.0f ? s_prev[z] / sc : 0.0f) : 1.0f;
 #pragma unroll
-                            for (uint32_t ni = 0; ni < 2; ni++) acc[mi][ni] *= r;
-                        s_prev = live ? sc : s_prev;
+                            for (uint32_t mi = 0; mi < 2; mi++)
+#pragma unroll
+                                for (uint32_t ni = 0; ni < 2; ni++)
+                                    if (!PM || ni == z) acc[mi][ni] *= r;
+                            s_prev[z] = live ? sc : s_prev[z];
+                        }
                     }
                     const Chunk &ch = ring[d];
 #pragma unroll
@@ -366,7 +415,7 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
                         bf16x8_t bw[2];
 #pragma unroll
                         for (uint32_t ni = 0; ni < 2; ni++)
-                            bw[ni] = e4m3x8_to_bf16x8_cvt(ch.b[ni][2 * q], ch.b[ni][2 * q + 1], keep);
+                            bw[ni] = e4m3x8_to_bf16x8_cvt(ch.b[ni][2 * q], ch.b[ni][2 * q + 1], keep[PM ? ni : 0]);
 #pragma unroll
                         for (uint32_t mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -384,7 +433,7 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
     float *red = reinterpret_cast<float *>(lds);
 #pragma unroll
     for (uint32_t a = 0; a < 4; a++) {
-        f32x16_t v = acc[a >> 1][a & 1] * s_prev;
+        f32x16_t v = acc[a >> 1][a & 1] * s_prev[PM ? (a & 1) : 0];
 #pragma unroll
         for (uint32_t r4 = 0; r4 < 4; r4++)
             *reinterpret_cast<float4 *>(red + ((wv * 4 + a) * 64 + lane) * 16 + 4 * r4) =
@@ -404,28 +453,58 @@ __device__ __forceinline__ void tail_tile(const GemmParams &p, uint32_t idx, uin
         for (uint32_t e = 0; e < 8; e++) sum[e] = w == 0 ? v[e] : sum[e] + v[e];
     }
     const uint32_t mi = a >> 1, ni = a & 1;
-    const uint32_t col = col0 + ni * 32 + (l & 31);
-    if (col < sg.rows) {
+    auto row_of = [&](uint32_t e) {
+        const uint32_t r = 8 * h + e;
+        return row0 + mi * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    };
+    if constexpr (PM == 2) {
+        // silu(segment 0) * segment 1: the segment-1 threads hand their sums
+        // to the segment-0 threads of the same lane and values through LDS
+        float *xu = reinterpret_cast<float *>(lds) + (mi * 64 + l) * 16 + 8 * h;
+        __syncthreads();   // every thread is done reading the partial tiles
+        if (ni == 1) {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) xu[e] = sum[e];
+        }
+        __syncthreads();
+        if (ni == 0) {
+            const uint32_t col = col0 + (l & 31);
+#pragma unroll
+            for (uint32_t e = 0; e < 8; e++) {
+                const uint32_t row = row_of(e);
+                const float y = row < p.m && col < sg.rows ? paired_swiglu(sum[e], xu[e]) : 0.0f;
+                store_act_bf16(p.act_out, p.act_kb, row, col, y);
+            }
+        }
+        return;
+    }
+    const GemmSeg &os = PM ? p.seg[ni] : sg;
+    const uint32_t col = col0 + (PM ? 0 : ni * 32) + (l & 31);
+    if (col < os.rows) {
 #pragma unroll
         for (uint32_t e = 0; e < 8; e++) {
-            const uint32_t r = 8 * h + e;
-            const uint32_t row = row0 + mi * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+            const uint32_t row = row_of(e);
             if (row < p.m) {
-                const size_t o = (size_t)row * sg.ldy + col;
-                sg.y[o] = sg.resid ? sg.resid[o] + sum[e] : sum[e];
+                const size_t o = (size_t)row * os.ldy + col;
+                os.y[o] = os.resid ? os.resid[o] + sum[e] : sum[e];
             }
         }
     }
 }
 
-template <bool MULTI>
+template <bool MULTI, uint32_t PM>
 __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tail_tile<MULTI>(p, blockIdx.x, lds);
+    tail_tile<MULTI, PM>(p, blockIdx.x, lds);
 }
 
-template <bool MULTI, bool NARROW>
+// PM (paired segments, GemmParams::pair): 0 -- none; 1 -- each tile holds
+// kTR/2 rows of segment 0 in its first half and the same rows of segment 1
+// in its second, fp32 outputs; 2 -- the same, writing silu(segment 0) *
+// segment 1 as bf16 activations (no K slices: the host plans none).
+template <bool MULTI, bool NARROW, uint32_t PM = 0>
 __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
+    static_assert(!(MULTI && PM), "paired tiles come from two segments of one shape");
     constexpr uint32_t kTM = 4, kTN = 2;   // 32x32 MFMA tiles per wavefront: 128 tokens x 64 rows
     using Geo = GemmGeo<NARROW>;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -447,6 +526,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // standard: 2 x 4 wavefronts of 128 x 64; narrow: 1 x 8
     const uint32_t wm = NARROW ? 0 : wv & 1, wn = NARROW ? wv : wv >> 1;
+    constexpr uint32_t kHW = (NARROW ? 8 : 4) / 2;   // paired: wn < kHW hold segment 0's rows
 
     // ---- global sources of this wavefront's pieces ----
     // A piece P (0 .. 4*kTM/32 - 1): token rows (mt*kTM/32 + P/4)*32..,
@@ -470,9 +550,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     for (uint32_t i = 0; i < Geo::kBL; i++) {
         const uint32_t Q = wv * Geo::kBL + i;
         const uint32_t n32 = Q / 2;
-        const uint32_t nbk = min(nt * Geo::kGroups + n32 / 4, sg.nb - 1);
-        boff[i] = nbk * KB * kBlockBytes + (n32 % 4) * kSubBytes + (Q % 2) * kChunkBytes;
+        // paired: 32-row groups [0, kTR/64) of segment 0, then the same of 1
+        const uint32_t n32p = PM && n32 >= Geo::kTR / 64 ? n32 - Geo::kTR / 64 : n32;
+        const uint32_t nbk = PM ? min(nt * (Geo::kGroups / 2) + n32p / 4, sg.nb - 1)
+                                : min(nt * Geo::kGroups + n32 / 4, sg.nb - 1);
+        boff[i] = nbk * KB * kBlockBytes + (n32p % 4) * kSubBytes + (Q % 2) * kChunkBytes;
     }
+    // paired: the groups one wavefront copies all lie in one segment's half
+    const uint8_t *bcodes = PM ? p.seg[wv * Geo::kBL / 2 >= Geo::kTR / 64 ? 1 : 0].codes : sg.codes;
     // Copy k of stage st into ring slot buf: k < kAL an A piece, then the
     // B pieces.
     auto issue_piece = [&](uint32_t st, uint32_t buf, uint32_t k) {
@@ -483,7 +568,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
                    la + (wv * Geo::kAL + k) * kChunkBytes);
         } else {
             const uint32_t i = k - Geo::kAL;
-            dma_1k(sg.codes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
+            dma_1k(bcodes + (boff[i] + kb * kBlockBytes + h * 2 * kChunkBytes + lane16),
                    la + Geo::kA + (wv * Geo::kBL + i) * kChunkBytes);
         }
     };
@@ -512,8 +597,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
             const uint32_t j0 = wv * 64 + i * kGemmThreads;   // the wavefront's first entry
             const uint32_t j = j0 + lane;
             const uint32_t g = j / Geo::kSliceKb, kk = min(j % Geo::kSliceKb, nkb - 1);
-            const uint32_t nbg = min(nt * Geo::kGroups + g, sg.nb - 1);
-            __builtin_amdgcn_global_load_lds(sg.scale + (size_t)nbg * KB + kb0 + kk, (lds_u8 *)(lds + kScaleOff) + j0 * 4,
+            const uint32_t gs = PM && g >= Geo::kGroups / 2 ? 1 : 0;   // paired: the group's segment
+            const uint32_t nbg = PM ? min(nt * (Geo::kGroups / 2) + g - gs * (Geo::kGroups / 2), sg.nb - 1)
+                                    : min(nt * Geo::kGroups + g, sg.nb - 1);
+            const float *gsc = PM ? (gs ? p.seg[1].scale : p.seg[0].scale) : sg.scale;
+            __builtin_amdgcn_global_load_lds(gsc + (size_t)nbg * KB + kb0 + kk, (lds_u8 *)(lds + kScaleOff) + j0 * 4,
                                              4, 0, 0);
         }
     }
@@ -694,27 +782,96 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     auto out_col = [&](uint32_t jn) -> uint32_t { return wn * (32 * kTN) + jn * 32 + (lane & 31); };
 
     if (!split) {
+        if constexpr (PM == 0) {
 #pragma unroll
-        for (uint32_t i = 0; i < kTM; i++)
+            for (uint32_t i = 0; i < kTM; i++)
 #pragma unroll
-            for (uint32_t jn = 0; jn < kTN; jn++)
+                for (uint32_t jn = 0; jn < kTN; jn++)
 #pragma unroll
-                for (uint32_t e = 0; e < 16; e++) {
-                    const uint32_t mrow = mt * Geo::kTM + out_row(i, e);
-                    const uint32_t ncol = nt * Geo::kTR + out_col(jn);
-                    if (mrow < p.m && ncol < sg.rows) {
-                        const size_t o = (size_t)mrow * sg.ldy + ncol;
-                        __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][e] : acc[i][jn][e],
-                                                    sg.y + o);
+                    for (uint32_t e = 0; e < 16; e++) {
+                        const uint32_t mrow = mt * Geo::kTM + out_row(i, e);
+                        const uint32_t ncol = nt * Geo::kTR + out_col(jn);
+                        if (mrow < p.m && ncol < sg.rows) {
+                            const size_t o = (size_t)mrow * sg.ldy + ncol;
+                            __builtin_nontemporal_store(sg.resid ? sg.resid[o] + acc[i][jn][e] : acc[i][jn][e],
+                                                        sg.y + o);
+                        }
                     }
-                }
+        } else {
+            // Paired: this wavefront holds rows of segment hs; its column
+            // within that segment's half of the tile.
+            const uint32_t hs = wn >= kHW ? 1 : 0;
+            auto pcol = [&](uint32_t jn) { return nt * (Geo::kTR / 2) + (wn - hs * kHW) * 64 + jn * 32 + (lane & 31); };
+            if constexpr (PM == 1) {
+                float *oy = hs ? p.seg[1].y : p.seg[0].y;
+#pragma unroll
+                for (uint32_t i = 0; i < kTM; i++)
+#pragma unroll
+                    for (uint32_t jn = 0; jn < kTN; jn++)
+#pragma unroll
+                        for (uint32_t e = 0; e < 16; e++) {
+                            const uint32_t mrow = mt * Geo::kTM + out_row(i, e);
+                            const uint32_t ncol = pcol(jn);
+                            if (mrow < p.m && ncol < sg.rows)
+                                __builtin_nontemporal_store(acc[i][jn][e], oy + (size_t)mrow * sg.ldy + ncol);
+                        }
+            } else {
+                // silu(segment 0) * segment 1.  The wavefronts (wm, wn) and
+                // (wm, wn + kHW) hold the same outputs of the two segments;
+                // segment 0's forms token sub-tiles 0 and 1 of the pair,
+                // segment 1's sub-tiles 2 and 3, each handing the other the
+                // accumulators it needs through LDS (the ring is free).
+                float *xch = reinterpret_cast<float *>(lds);
+                const uint32_t pi = wm * kHW + (wn - hs * kHW);
+                auto xat = [&](uint32_t side, uint32_t t4, uint32_t e) -> float & {
+                    return xch[(((pi * 2 + side) * 4 + t4) * 16 + e) * 64 + lane];
+                };
+                auto hand_over = [&](auto basec) {   // accumulators basec, basec + 1 into side hs
+                    constexpr uint32_t base = decltype(basec)::value;
+#pragma unroll
+                    for (uint32_t ii = 0; ii < 2; ii++)
+#pragma unroll
+                        for (uint32_t jn = 0; jn < kTN; jn++)
+#pragma unroll
+                            for (uint32_t e = 0; e < 16; e++) xat(hs, ii * 2 + jn, e) = acc[base + ii][jn][e];
+                };
+                auto form = [&](auto basec) {   // sub-tiles basec, basec + 1 with the other side's values
+                    constexpr uint32_t base = decltype(basec)::value;
+#pragma unroll
+                    for (uint32_t ii = 0; ii < 2; ii++)
+#pragma unroll
+                        for (uint32_t jn = 0; jn < kTN; jn++)
+#pragma unroll
+                            for (uint32_t e = 0; e < 16; e++) {
+                                const float own = acc[base + ii][jn][e], other = xat(1 - hs, ii * 2 + jn, e);
+                                const uint32_t mrow = mt * Geo::kTM + out_row(base + ii, e);
+                                const uint32_t ncol = pcol(jn);
+                                if (ncol < p.act_kb * kBlock)
+                                    store_act_bf16(p.act_out, p.act_kb, mrow, ncol,
+                                                   mrow < p.m && ncol < sg.rows
+                                                       ? paired_swiglu(hs ? other : own, hs ? own : other)
+                                                       : 0.0f);
+                            }
+                };
+                __syncthreads();   // every wavefront is done reading the ring
+                if (hs)
+                    hand_over(std::integral_constant<uint32_t, 0>{});
+                else
+                    hand_over(std::integral_constant<uint32_t, 2>{});
+                __syncthreads();
+                if (hs)
+                    form(std::integral_constant<uint32_t, 2>{});
+                else
+                    form(std::integral_constant<uint32_t, 0>{});
+            }
+        }
         // One 64x64 tile of the last round's tail, while these stores drain
         // (every workgroup reaches this point at about the same time, when
         // the device's write bandwidth bounds the stores).
         if constexpr (!NARROW) {
             if (blockIdx.x < p.tail_fused) {
                 __syncthreads();   // the ring is free: every wavefront is past its last LDS read
-                tail_tile<MULTI>(p, blockIdx.x, lds);
+                tail_tile<MULTI, PM>(p, blockIdx.x, lds);
             }
         }
         return;
@@ -741,9 +898,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
 // Ordered sum of the K slices of split tiles: y = ((p_0 + p_1) + p_2) + ...
 // One thread per float4 of a partial tile (16384 per tile); the layout is
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
-// the partials are visible without any device-scope protocol.
-template <bool MULTI, bool NARROW>
+// the partials are visible without any device-scope protocol.  PM = 1:
+// paired tiles (fp32 outputs), whose second half of columns belongs to
+// segment 1.
+template <bool MULTI, bool NARROW, uint32_t PM = 0>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+    static_assert(PM < 2, "paired tiles with activation outputs are never cut along K");
     using Geo = GemmGeo<NARROW>;
     constexpr uint32_t kTileQuads = kGemmTile * kGemmTile / 4;
     const uint32_t f = blockIdx.x * 256 + threadIdx.x;
@@ -758,8 +918,11 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const TileAt ta = tile_at<MULTI>(p, tile);
     const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
     if (row0 >= p.m) return;   // padding rows: never stored by the slices
-    const GemmSeg &sg = p.seg[ta.seg];
-    const uint32_t col = ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
+    constexpr uint32_t kHW = (NARROW ? 8 : 4) / 2;
+    const uint32_t hs = PM && wn >= kHW ? 1 : 0;
+    const GemmSeg &sg = p.seg[PM ? hs : ta.seg];
+    const uint32_t col = PM ? ta.nt * (Geo::kTR / 2) + (wn - hs * kHW) * 64 + jn * 32 + (lane & 31)
+                            : ta.nt * Geo::kTR + wn * 64 + jn * 32 + (lane & 31);
     // The residuals (y may be the residual, updated in place) are loaded
     // first, all four together with the rows and the column clamped in
     // bounds: loaded one by one between the stores, each waited for the
@@ -864,14 +1027,14 @@ static bool fuse_tail() {
     return on;
 }
 
-template <bool MULTI, bool NARROW>
+template <bool MULTI, bool NARROW, uint32_t PM = 0>
 static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel<MULTI, NARROW>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_fp8_kernel<MULTI, NARROW, PM>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
         if (e == hipSuccess && !NARROW)
-            e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel<MULTI>),
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_tail_kernel<MULTI, PM>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTailLds);
         if (e != hipSuccess) return e;
         attr_set = true;
@@ -879,26 +1042,38 @@ static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     if (NARROW && p.tail_tile0 != p.mtiles * p.ntiles) return hipErrorInvalidValue;   // no 64x64 tail
     const uint32_t tiles = p.mtiles * p.ntiles;
     const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
+    if (PM == 2 && nsplit) return hipErrorInvalidValue;    // activation outputs: whole and 64x64 tiles only
     const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
     const uint32_t ntail = (tiles - p.tail_tile0) * kTailPerTile;   // 64x64 tiles
     GemmParams q = p;
     // the 64x64 tiles run in the whole-tile workgroups, after their stores
     q.tail_fused = (ntail && !nsplit && p.split_tile0 >= ntail && fuse_tail()) ? ntail : 0;
     if (grid)
-        hipLaunchKernelGGL((gemm_fp8_kernel<MULTI, NARROW>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
+        hipLaunchKernelGGL((gemm_fp8_kernel<MULTI, NARROW, PM>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
     if (nsplit) {
         const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
-        hipLaunchKernelGGL((gemm_reduce_kernel<MULTI, NARROW>), dim3(quads / 256), dim3(256), 0, stream, p);
+        if constexpr (PM < 2)
+            hipLaunchKernelGGL((gemm_reduce_kernel<MULTI, NARROW, PM>), dim3(quads / 256), dim3(256), 0, stream, p);
     }
     if constexpr (!NARROW) {
         if (ntail && !q.tail_fused)
-            hipLaunchKernelGGL(gemm_tail_kernel<MULTI>, dim3(ntail), dim3(kGemmThreads), kTailLds, stream, q);
+            hipLaunchKernelGGL((gemm_tail_kernel<MULTI, PM>), dim3(ntail), dim3(kGemmThreads), kTailLds, stream, q);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.nseg == 0 || p.nseg > 4) return hipErrorInvalidValue;
+    if (p.pair) {
+        const GemmSeg &a = p.seg[0], &b = p.seg[1];
+        if (p.nseg != 2 || a.rows != b.rows || a.nb != b.nb || a.ldy != b.ldy || a.resid || b.resid)
+            return hipErrorInvalidValue;
+        if (p.act_out) {   // standard tiles only (the narrow plan always cuts along K)
+            if (p.narrow || p.act_kb != a.nb) return hipErrorInvalidValue;
+            return launch_gemm_t<false, false, 2>(p, stream);
+        }
+        return p.narrow ? launch_gemm_t<false, true, 1>(p, stream) : launch_gemm_t<false, false, 1>(p, stream);
+    }
     if (p.narrow) return p.nseg > 1 ? launch_gemm_t<true, true>(p, stream) : launch_gemm_t<false, true>(p, stream);
     return p.nseg > 1 ? launch_gemm_t<true, false>(p, stream) : launch_gemm_t<false, false>(p, stream);
 }

@@ -128,6 +128,7 @@ struct Device {
     bool done_spin = true;      // Q35MM_HOST_WAIT=sync: hipStreamSynchronize instead
     uint32_t gemm_min_m = 64;
     bool gemm_narrow = true;    // Q35MM_GEMM_NARROW=0: 256-token tiles for every m
+    bool gemm_pair = true;      // Q35MM_GEMM_PAIR=0: two weights of one shape as separate tiles
     uint32_t cus = 256;
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
@@ -161,6 +162,7 @@ int ensure_device() {
     g_dev.id = dev;
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.gemm_narrow = env_u32("Q35MM_GEMM_NARROW", 1) != 0;
+    g_dev.gemm_pair = env_u32("Q35MM_GEMM_PAIR", 1) != 0;
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
     {
         const char *v = getenv("Q35MM_VERIFY_WEIGHTS");
@@ -561,9 +563,26 @@ struct GemmNorm {
     float eps;
 };
 
+// Two weights of one shape (gate and up) run as paired tiles, each holding
+// the same rows of both; with a GemmAct the tiles write silu(weight 0) *
+// weight 1 straight into the next GEMM's bf16 activations (buf: rows_pad x
+// nb*128 of gemm_act_bytes) when the plan has no K slices, and done says so
+// (otherwise they wrote the fp32 outputs).
+struct GemmAct {
+    uint16_t *buf;
+    bool done;
+};
+size_t gemm_act_bytes(uint32_t m, uint32_t cols) {
+    const uint32_t tile_m = m <= kGemmNarrowMaxM && g_dev.gemm_narrow ? kGemmNarrowMaxM : kGemmTile;
+    return (size_t)(m + tile_m - 1) / tile_m * tile_m * ((cols + kBlock - 1) / kBlock) * kBlock * sizeof(uint16_t);
+}
+
+// xb_ready: the activations already in the GEMM's bf16 layout (a paired
+// GEMM's GemmAct output), so no conversion runs and dX is not read.
 int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const float *dX, float *const *dY,
              hipStream_t st, const float *const *resid = nullptr, const float *x2 = nullptr,
-             Scratch *scr = nullptr, const GemmNorm *norm = nullptr) {
+             Scratch *scr = nullptr, const GemmNorm *norm = nullptr, GemmAct *act = nullptr,
+             const uint16_t *xb_ready = nullptr) {
     const Weight &w0 = wt[0]->w;
     Scratch &sc = scr ? *scr : scratch_for(st);
     for (uint32_t s = 0; s < nseg; s++) {
@@ -574,6 +593,10 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         if (!gemm_fits(w, m))
             return set_error(Q35MM_EINVAL, "GEMM operands exceed 4 GiB (m=%u, %ux%u)", m, w.rows, w.cols);
     }
+    // Two weights of one shape: paired tiles (the first half of a tile's
+    // rows from weight 0, the same rows of weight 1 in the second half).
+    const bool pair = nseg == 2 && g_dev.gemm_pair && !resid && !x2 && wt[0]->w.rows == wt[1]->w.rows &&
+                      wt[0]->w.nb == wt[1]->w.nb;
     // Up to 128 tokens: tiles of 128 tokens x 512 rows (4 row groups), whose
     // partial round is cut along K -- unless those partials would not fit
     // the fixed scratch of an allocation-free call, which then keeps the
@@ -581,7 +604,10 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     auto plan_for = [&](bool narrow, uint32_t &groups, size_t &xb_bytes) {
         groups = narrow ? kGemmNarrowRows / kBlock : kGemmTile / kBlock;
         uint32_t ntiles = 0;
-        for (uint32_t s = 0; s < nseg; s++) ntiles += (wt[s]->w.nb + groups - 1) / groups;
+        if (pair)
+            ntiles = (w0.nb + groups / 2 - 1) / (groups / 2);
+        else
+            for (uint32_t s = 0; s < nseg; s++) ntiles += (wt[s]->w.nb + groups - 1) / groups;
         const GemmPlan pl = gemm_plan(m, ntiles, w0.kb, g_dev.cus, narrow);
         xb_bytes = (size_t)pl.mtiles * (narrow ? kGemmNarrowMaxM : kGemmTile) * w0.kb * kBlock * sizeof(uint16_t);
         return pl;
@@ -597,8 +623,11 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     const uint32_t tile_m = narrow ? kGemmNarrowMaxM : kGemmTile;
     uint16_t *xb = nullptr;
     float *ws = nullptr;
-    const int rc = scratch_gemm(sc, xb_bytes, pl.ws_bytes(), &xb, &ws);
+    const int rc = scratch_gemm(sc, xb_ready ? 0 : xb_bytes, pl.ws_bytes(), &xb, &ws);
     if (rc) return rc;
+    if (xb_ready) xb = const_cast<uint16_t *>(xb_ready);
+    const bool act_out = pair && act && act->buf && !narrow && pl.split_tile0 == pl.tail_tile0;
+    if (act) act->done = act_out;
     GemmParams p{};
     uint32_t tile0 = 0;
     for (uint32_t s = 0; s < nseg; s++) {
@@ -611,9 +640,12 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
         g.rows = w.rows;
         g.ldy = w.rows;
         g.nb = w.nb;
-        g.tile0 = tile0;
+        g.tile0 = pair ? 0 : tile0;
         tile0 += pl.mtiles * ((w.nb + groups - 1) / groups);
     }
+    p.pair = pair ? 1u : 0u;
+    p.act_out = act_out ? act->buf : nullptr;
+    p.act_kb = act_out ? w0.nb : 0u;
     p.nseg = nseg;
     p.xb = xb;
     p.ws = ws;
@@ -625,10 +657,13 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     p.nslices = pl.nslices;
     p.tail_tile0 = pl.tail_tile0;
     p.narrow = narrow ? 1u : 0u;
-    if (norm)
+    if (xb_ready) {
+        // activations written by the previous GEMM
+    } else if (norm) {
         HIP_TRY(launch_rmsnorm_bf16(dX, w0.cols, norm->w, m, w0.cols, norm->eps, pl.mtiles * tile_m, w0.kb, xb, st));
-    else
+    } else {
         HIP_TRY(launch_act_to_bf16(dX, x2, w0.cols, m, w0.cols, pl.mtiles * (tile_m / kSubRows), w0.kb, xb, st));
+    }
     HIP_TRY(launch_gemm(p, st));
     return Q35MM_OK;
 }
@@ -1538,11 +1573,14 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
                          gate->w.cols, up->w.rows, up->w.cols, down->w.rows, down->w.cols);
     if (m == 0) return Q35MM_OK;
     if (!dX || !dNormW) return set_error(Q35MM_EINVAL, "null pointer");
-    // workspace: xn [m][H], g [m][I], u [m][I], y [m][H]; SwiGLU writes g in place
+    // workspace: xn [m][H], g [m][I], u [m][I], y [m][H] (SwiGLU writes g in
+    // place), then the down GEMM's bf16 activations when the gate+up GEMM
+    // forms them
     const size_t nh = (size_t)m * H, ni = (size_t)m * I;
     hipStream_t st = pick_stream(stream);
     Scratch &scr = scratch_for(st);
-    rc = grow(scr.mlp, (2 * nh + 2 * ni) * sizeof(float), false, &scr);
+    const size_t act_off = ((2 * nh + 2 * ni) * sizeof(float) + 255) & ~(size_t)255;
+    rc = grow(scr.mlp, act_off + gemm_act_bytes(m, I), false, &scr);
     if (rc) return rc;
     float *xn = (float *)scr.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     const bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(gate->w, m) &&
@@ -1603,24 +1641,28 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
         HIP_TRY(launch_add_inplace(dX, y, nh, st));
         return Q35MM_OK;
     }
-    // Prefill: gate and up as one GEMM launch, the RMSNorm written straight
-    // into its bf16 activations (a separate RMSNorm kernel and fp32 rows
-    // when the row length or alignment does not suit that kernel); the down
-    // GEMM forms silu(gate) * up while rounding its activations to bf16 and
-    // adds the residual in its epilogue (the bits of the separate calls).
+    // Prefill: gate and up as one GEMM launch of paired tiles, the RMSNorm
+    // written straight into its bf16 activations (a separate RMSNorm kernel
+    // and fp32 rows when the row length or alignment does not suit that
+    // kernel), the tiles forming silu(gate) * up as the down GEMM's bf16
+    // activations (when the plan cuts no tile along K; otherwise the down
+    // GEMM forms it while rounding its activations), the down GEMM adding
+    // the residual in its epilogue -- the bits of the separate calls.
     const q35mm_weight *gu[2] = {gate, up};
     float *gy[2] = {g, u};
+    GemmAct act{reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(scr.mlp.ptr) + act_off), false};
     if (rmsnorm_bf16_fits(dX, H, dNormW, H)) {
         const GemmNorm nm{dNormW, eps};
-        rc = run_gemm(gu, 2, m, dX, gy, st, nullptr, nullptr, nullptr, &nm);
+        rc = run_gemm(gu, 2, m, dX, gy, st, nullptr, nullptr, nullptr, &nm, &act);
     } else {
         HIP_TRY(launch_rmsnorm(dX, H, dNormW, xn, H, m, H, eps, st));
-        rc = run_gemm(gu, 2, m, xn, gy, st);
+        rc = run_gemm(gu, 2, m, xn, gy, st, nullptr, nullptr, nullptr, nullptr, &act);
     }
     if (rc) return rc;
     const q35mm_weight *dn[1] = {down};
     float *dy[1] = {dX};
     const float *res[1] = {dX};
+    if (act.done) return run_gemm(dn, 1, m, nullptr, dy, st, res, nullptr, nullptr, nullptr, nullptr, act.buf);
     return run_gemm(dn, 1, m, g, dy, st, res, u);
 }
 

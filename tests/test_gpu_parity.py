@@ -316,6 +316,28 @@ def test_gemm_multi_segment(q, oracle, wl, gpu, m):
         w.free()
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 1000, 3000), (200, 1000, 3000), (200, 1000, 1000), (300, 256, 16640)])
+def test_gemm_multi_two_weights_of_one_shape(q, oracle, wl, gpu, m, k, n):
+    """Two weights of one shape (the MLP's gate and up) on the GEMM path run
+    as paired tiles, each holding the same rows of both weights: narrow tiles
+    cut along K (64 tokens), 256 x 256 tiles cut along K (200 x 3000), only
+    64x64 tiles (200 x 1000), whole tiles with padding tokens and a fused
+    64x64 tail (300 x 16640).  Each output within the GEMM bars of the
+    oracle."""
+    import torch
+    Ws = [wl.gen_weight(0x9A1 + i + n, n, k) for i in range(2)]
+    X = wl.gen_act(0x9A3 + m, m, k)
+    ws = [q.Weight(*w) for w in Ws]
+    Ys = [torch.empty((m, n), dtype=torch.float32, device=gpu) for _ in ws]
+    q.matmul_multi(ws, _torch_dev(X, gpu), Ys)
+    torch.cuda.synchronize()
+    for (W, sc), Y in zip(Ws, Ys):
+        rel, mx = _gemm_check(Y.cpu().numpy(), oracle.mm_batch(W, sc, X))
+        assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (W.shape, rel, mx)
+    for w in ws:
+        w.free()
+
+
 def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
     """Blocks whose scale is 0 contribute nothing (the reference's
     lut[code] * 0): first K blocks of a row group, blocks in the middle and a
