@@ -912,9 +912,9 @@ def main():
         mlp_out["prefill_m512"] = {"us_per_block": round(el_p / reps_p * 1e6, 2),
                                    "TFLOPs": round(flops_p * reps_p / el_p / 1e12, 1),
                                    "note": "q35mm_mlp at 512 tokens: the RMSNorm written straight into the bf16 "
-                                           "activations of one GEMM launch over gate and up, the down GEMM "
-                                           "forming SwiGLU while rounding its activations to bf16 and adding the "
-                                           "residual in its epilogue"}
+                                           "activations of one GEMM launch over gate and up, whose paired tiles "
+                                           "write silu(gate) * up as the down GEMM's bf16 activations, the down "
+                                           "GEMM adding the residual in its epilogue"}
         log(f"mlp block: {mlp_out}")
 
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----
