@@ -1579,12 +1579,12 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
     const size_t nh = (size_t)m * H, ni = (size_t)m * I;
     hipStream_t st = pick_stream(stream);
     Scratch &scr = scratch_for(st);
-    const size_t act_off = ((2 * nh + 2 * ni) * sizeof(float) + 255) & ~(size_t)255;
-    rc = grow(scr.mlp, act_off + gemm_act_bytes(m, I), false, &scr);
-    if (rc) return rc;
-    float *xn = (float *)scr.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     const bool gemm = m >= g_dev.gemm_min_m && g_dev.gemm_min_m > 0 && gemm_fits(gate->w, m) &&
                       gemm_fits(up->w, m) && gemm_fits(down->w, m);
+    const size_t act_off = ((2 * nh + 2 * ni) * sizeof(float) + 255) & ~(size_t)255;
+    rc = grow(scr.mlp, act_off + (gemm ? gemm_act_bytes(m, I) : 0), false, &scr);
+    if (rc) return rc;
+    float *xn = (float *)scr.mlp.ptr, *g = xn + nh, *u = g + ni, *y = u + ni;
     if (!gemm) {
         // Decode.  RMSNorm inside the gate+up GEMV when a group's rows fit
         // its registers (each workgroup forms the sums of squares itself),

@@ -364,6 +364,40 @@ def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
     assert (Y[:, 256:384] == 0).all()
 
 
+@pytest.mark.parametrize("m", [96, 200])
+def test_gemm_paired_zero_scale_blocks(q, oracle, wl, gpu, m):
+    """Paired tiles of two weights whose zero-scale blocks differ (each
+    weight's block scales tracked on their own): narrow tiles cut along K
+    (96 tokens) and 64x64 tiles only (200).  Within the GEMM bars of the
+    oracle; a row group with no live block exactly 0 in its own weight
+    only."""
+    import torch
+    k, n = 1536, 640
+    rng = np.random.default_rng(95)
+    Ws, scs = [], []
+    for i in range(2):
+        W = rng.integers(0, 0x7E, size=(n, k), dtype=np.uint8) | (rng.integers(0, 2, size=(n, k), dtype=np.uint8) << 7)
+        sc = np.full((n // 128, k // 128), 0x3980, np.uint16)       # bf16 2^-12: outputs of unit scale
+        Ws.append(W)
+        scs.append(sc)
+    scs[0][0, 0] = 0                  # first block of group 0, weight 0 only
+    scs[1][1, 5:7] = 0                # middle blocks of group 1, weight 1 only
+    scs[0][2, :] = 0                  # group 2 dead in weight 0, live in weight 1
+    scs[1][3, -1] = 0                 # last block of group 3, weight 1 only
+    X = wl.gen_act(96, m, k)
+    ws = [q.Weight(W, sc) for W, sc in zip(Ws, scs)]
+    Ys = [torch.empty((m, n), dtype=torch.float32, device=gpu) for _ in ws]
+    q.matmul_multi(ws, _torch_dev(X, gpu), Ys)
+    torch.cuda.synchronize()
+    for W, sc, dY in zip(Ws, scs, Ys):
+        rel, mx = _gemm_check(dY.cpu().numpy(), oracle.mm_batch(W, sc, X))
+        assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (rel, mx)
+    assert (Ys[0].cpu().numpy()[:, 256:384] == 0).all()
+    assert (Ys[1].cpu().numpy()[:, 256:384] != 0).any()
+    for w in ws:
+        w.free()
+
+
 @pytest.mark.parametrize("m", [64, 200])
 def test_gemm_k_beyond_one_slice_table(q, oracle, wl, gpu, m):
     """K of 1025 blocks: more than one workgroup's LDS scale table (1024
