@@ -33,6 +33,12 @@
 //    when there is no whole round), or cut along K, their partial tiles added
 //    in slice order by a second kernel (deterministic, spread over the whole
 //    device).
+//  - Two weights of one shape (the MLP's gate and up) run as paired tiles:
+//    the first half of a tile's rows from one, the same rows of the other in
+//    the second half, so each output of one sits in the same workgroup as the
+//    same output of the other.  The MLP block uses that to form silu(gate) *
+//    up in the epilogue and write it, rounded to bf16, as the down GEMM's
+//    activations.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
