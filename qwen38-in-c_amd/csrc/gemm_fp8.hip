@@ -807,7 +807,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
             // Paired: this wavefront holds rows of segment hs; its column
             // within that segment's half of the tile.
             const uint32_t hs = wn >= kHW ? 1 : 0;
-            auto pcol = [&](uint32_t jn) { return nt * (Geo::kTR / 2) + (wn - hs * kHW) * 64 + jn * 32 + (lane & 31); };
+            auto pcol = [&](uint32_t jn) {
+                return nt * (Geo::kTR / 2) + (wn - hs * kHW) * 64 + jn * 32 + (lane & 31);
+            };
             if constexpr (PM == 1) {
                 float *oy = hs ? p.seg[1].y : p.seg[0].y;
 #pragma unroll
