@@ -897,24 +897,25 @@ def main():
                                "RMSNorm and SwiGLU as their own kernels (gate, up and down run the row-split "
                                "GEMV, which takes plain activations), the residual add inside the down GEMV")
                             + "; us_matmuls_only = the gate+up and down GEMV launches on ready activations")}
-        # the same block on the prefill path: 512 tokens, gate and up as one
-        # GEMM launch over both weights, SwiGLU and the residual add as kernels
-        mp = 512
-        xres_p = torch.randn((mp, H), device=dev, generator=gen)
+        # the same block on the prefill path: 512 tokens (256 x 256 tiles) and
+        # 128 (a short prompt: 128 x 512 tiles cut along K)
+        for mp in (512, 128):
+            xres_p = torch.randn((mp, H), device=dev, generator=gen)
 
-        def block_p(i):
-            L = layers[i % args.pool]
-            q.mlp(L[GATE], L[UP], L[4], nws[i % args.pool], xres_p)
-        reps_p = max(args.pool, args.prefill_reps // args.pool * args.pool)
-        el_p, gp = time_graph(torch, block_p, reps_p, 2, not args.eager)
-        del gp
-        flops_p = 2 * mp * H * I * 3
-        mlp_out["prefill_m512"] = {"us_per_block": round(el_p / reps_p * 1e6, 2),
-                                   "TFLOPs": round(flops_p * reps_p / el_p / 1e12, 1),
-                                   "note": "q35mm_mlp at 512 tokens: the RMSNorm written straight into the bf16 "
-                                           "activations of one GEMM launch over gate and up, whose paired tiles "
-                                           "write silu(gate) * up as the down GEMM's bf16 activations, the down "
-                                           "GEMM adding the residual in its epilogue"}
+            def block_p(i):
+                L = layers[i % args.pool]
+                q.mlp(L[GATE], L[UP], L[4], nws[i % args.pool], xres_p)
+            reps_p = max(args.pool, args.prefill_reps // args.pool * args.pool)
+            el_p, gp = time_graph(torch, block_p, reps_p, 2, not args.eager)
+            del gp
+            flops_p = 2 * mp * H * I * 3
+            mlp_out[f"prefill_m{mp}"] = {
+                "us_per_block": round(el_p / reps_p * 1e6, 2),
+                "TFLOPs": round(flops_p * reps_p / el_p / 1e12, 1),
+                "note": f"q35mm_mlp at {mp} tokens: the RMSNorm written straight into the bf16 activations of one "
+                        "GEMM launch over gate and up, whose paired tiles (or, for tiles cut along K, their slice "
+                        "sum) write silu(gate) * up as the down GEMM's bf16 activations, the down GEMM adding the "
+                        "residual in its epilogue or slice sum"}
         log(f"mlp block: {mlp_out}")
 
     # ---- decode sweep M = 1, 2, 4, 8 (per shape) ----

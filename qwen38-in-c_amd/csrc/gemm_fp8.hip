@@ -507,7 +507,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tail_kernel(GemmParams p) {
 // PM (paired segments, GemmParams::pair): 0 -- none; 1 -- each tile holds
 // kTR/2 rows of segment 0 in its first half and the same rows of segment 1
 // in its second, fp32 outputs; 2 -- the same, writing silu(segment 0) *
-// segment 1 as bf16 activations (no K slices: the host plans none).
+// segment 1 as bf16 activations (split tiles publish partials as usual and
+// gemm_reduce_kernel<..., 2> forms the products).
 template <bool MULTI, bool NARROW, uint32_t PM = 0>
 __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
     static_assert(!(MULTI && PM), "paired tiles come from two segments of one shape");
@@ -908,10 +909,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_fp8_kernel(GemmParams p) {
 // the one gemm_fp8_kernel publishes.  Runs after it on the same stream, so
 // the partials are visible without any device-scope protocol.  PM = 1:
 // paired tiles (fp32 outputs), whose second half of columns belongs to
-// segment 1.
+// segment 1; PM = 2: the same tiles forming silu(segment 0) * segment 1 as
+// bf16 activations.
 template <bool MULTI, bool NARROW, uint32_t PM = 0>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
-    static_assert(PM < 2, "paired tiles with activation outputs are never cut along K");
     using Geo = GemmGeo<NARROW>;
     constexpr uint32_t kTileQuads = kGemmTile * kGemmTile / 4;
     const uint32_t f = blockIdx.x * 256 + threadIdx.x;
@@ -925,8 +926,52 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
     const uint32_t i = q >> 3, jn = (q >> 2) & 1, r4 = q & 3;
     const TileAt ta = tile_at<MULTI>(p, tile);
     const uint32_t row0 = ta.mt * Geo::kTM + wm * 128 + i * 32 + 8 * r4 + 4 * (lane >> 5);
-    if (row0 >= p.m) return;   // padding rows: never stored by the slices
     constexpr uint32_t kHW = (NARROW ? 8 : 4) / 2;
+    if constexpr (PM == 2) {
+        // The threads of segment 0's columns sum both segments' partials
+        // (segment 1's float4 of the same outputs sits kGemmThreads / 2
+        // threads further in the layout), in slice order as below, and
+        // write four tokens of one column; padding tokens and columns past
+        // the weight's rows as zeros.
+        if (wn >= kHW) return;
+        const uint32_t col = ta.nt * (Geo::kTR / 2) + wn * 64 + jn * 32 + (lane & 31);
+        if (col >= p.act_kb * kBlock) return;
+        float y[4] = {};
+        if (row0 < p.m && col < p.seg[0].rows) {
+            const float4 *pg = reinterpret_cast<const float4 *>(p.ws) + (size_t)st * S * kTileQuads + fq;
+            const float4 *pu = pg + kGemmThreads / 2;
+            float4 vg[4], vu[4];
+            float4 tg = pg[0], tu = pu[0];
+            for (uint32_t s0 = 1; s0 < S; s0 += 4) {
+#pragma unroll
+                for (uint32_t b = 0; b < 4; b++)
+                    if (s0 + b < S) {
+                        vg[b] = pg[(size_t)(s0 + b) * kTileQuads];
+                        vu[b] = pu[(size_t)(s0 + b) * kTileQuads];
+                    }
+#pragma unroll
+                for (uint32_t b = 0; b < 4; b++)
+                    if (s0 + b < S) {
+                        tg.x += vg[b].x;
+                        tg.y += vg[b].y;
+                        tg.z += vg[b].z;
+                        tg.w += vg[b].w;
+                        tu.x += vu[b].x;
+                        tu.y += vu[b].y;
+                        tu.z += vu[b].z;
+                        tu.w += vu[b].w;
+                    }
+            }
+            const float g4[4] = {tg.x, tg.y, tg.z, tg.w}, u4[4] = {tu.x, tu.y, tu.z, tu.w};
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++)
+                if (row0 + e < p.m) y[e] = paired_swiglu(g4[e], u4[e]);
+        }
+#pragma unroll
+        for (uint32_t e = 0; e < 4; e++) store_act_bf16(p.act_out, p.act_kb, row0 + e, col, y[e]);
+        return;
+    }
+    if (row0 >= p.m) return;   // padding rows: never stored by the slices
     const uint32_t hs = PM && wn >= kHW ? 1 : 0;
     const GemmSeg &sg = p.seg[PM ? hs : ta.seg];
     const uint32_t col = PM ? ta.nt * (Geo::kTR / 2) + (wn - hs * kHW) * 64 + jn * 32 + (lane & 31)
@@ -1050,7 +1095,6 @@ static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
     if (NARROW && p.tail_tile0 != p.mtiles * p.ntiles) return hipErrorInvalidValue;   // no 64x64 tail
     const uint32_t tiles = p.mtiles * p.ntiles;
     const uint32_t nsplit = p.tail_tile0 - p.split_tile0;   // tiles cut along K
-    if (PM == 2 && nsplit) return hipErrorInvalidValue;    // activation outputs: whole and 64x64 tiles only
     const uint32_t grid = p.split_tile0 + nsplit * p.nslices;
     const uint32_t ntail = (tiles - p.tail_tile0) * kTailPerTile;   // 64x64 tiles
     GemmParams q = p;
@@ -1060,8 +1104,7 @@ static hipError_t launch_gemm_t(const GemmParams &p, hipStream_t stream) {
         hipLaunchKernelGGL((gemm_fp8_kernel<MULTI, NARROW, PM>), dim3(grid), dim3(kGemmThreads), kGemmLds, stream, q);
     if (nsplit) {
         const uint32_t quads = nsplit * (kGemmTile * kGemmTile / 4);
-        if constexpr (PM < 2)
-            hipLaunchKernelGGL((gemm_reduce_kernel<MULTI, NARROW, PM>), dim3(quads / 256), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((gemm_reduce_kernel<MULTI, NARROW, PM>), dim3(quads / 256), dim3(256), 0, stream, p);
     }
     if constexpr (!NARROW) {
         if (ntail && !q.tail_fused)
@@ -1076,9 +1119,9 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
         const GemmSeg &a = p.seg[0], &b = p.seg[1];
         if (p.nseg != 2 || a.rows != b.rows || a.nb != b.nb || a.ldy != b.ldy || a.resid || b.resid)
             return hipErrorInvalidValue;
-        if (p.act_out) {   // standard tiles only (the narrow plan always cuts along K)
-            if (p.narrow || p.act_kb != a.nb) return hipErrorInvalidValue;
-            return launch_gemm_t<false, false, 2>(p, stream);
+        if (p.act_out) {
+            if (p.act_kb != a.nb) return hipErrorInvalidValue;
+            return p.narrow ? launch_gemm_t<false, true, 2>(p, stream) : launch_gemm_t<false, false, 2>(p, stream);
         }
         return p.narrow ? launch_gemm_t<false, true, 1>(p, stream) : launch_gemm_t<false, false, 1>(p, stream);
     }

@@ -239,9 +239,9 @@ struct GemmParams {
     uint32_t narrow;     // tiles of 128 tokens x 512 rows (m <= 128) instead of 256 x 256
     // Paired segments (nseg == 2, equal shapes): each tile holds rows r..r+T/2
     // of segment 0 in its first half and the same rows of segment 1 in its
-    // second (ntiles counts such tiles).  With act_out (whole and 64x64 tiles
-    // only, no K slices) the tile writes silu(seg 0) * seg 1 as bf16 in the
-    // lane-order activation layout of act_kb K blocks instead of fp32 y.
+    // second (ntiles counts such tiles).  With act_out the tiles (or, for
+    // tiles cut along K, the slice sum) write silu(seg 0) * seg 1 as bf16 in
+    // the lane-order activation layout of act_kb K blocks instead of fp32 y.
     uint32_t pair;
     uint16_t *act_out;
     uint32_t act_kb;

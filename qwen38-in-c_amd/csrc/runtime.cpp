@@ -566,8 +566,8 @@ struct GemmNorm {
 // Two weights of one shape (gate and up) run as paired tiles, each holding
 // the same rows of both; with a GemmAct the tiles write silu(weight 0) *
 // weight 1 straight into the next GEMM's bf16 activations (buf: rows_pad x
-// nb*128 of gemm_act_bytes) when the plan has no K slices, and done says so
-// (otherwise they wrote the fp32 outputs).
+// nb*128 of gemm_act_bytes), and done says so (when the weights do not
+// pair, they wrote the fp32 outputs).
 struct GemmAct {
     uint16_t *buf;
     bool done;
@@ -626,7 +626,7 @@ int run_gemm(const q35mm_weight *const *wt, uint32_t nseg, uint32_t m, const flo
     const int rc = scratch_gemm(sc, xb_ready ? 0 : xb_bytes, pl.ws_bytes(), &xb, &ws);
     if (rc) return rc;
     if (xb_ready) xb = const_cast<uint16_t *>(xb_ready);
-    const bool act_out = pair && act && act->buf && !narrow && pl.split_tile0 == pl.tail_tile0;
+    const bool act_out = pair && act && act->buf;
     if (act) act->done = act_out;
     GemmParams p{};
     uint32_t tile0 = 0;
@@ -1644,10 +1644,10 @@ Q35MM_API int q35mm_mlp(const q35mm_weight *gate, const q35mm_weight *up, const 
     // Prefill: gate and up as one GEMM launch of paired tiles, the RMSNorm
     // written straight into its bf16 activations (a separate RMSNorm kernel
     // and fp32 rows when the row length or alignment does not suit that
-    // kernel), the tiles forming silu(gate) * up as the down GEMM's bf16
-    // activations (when the plan cuts no tile along K; otherwise the down
-    // GEMM forms it while rounding its activations), the down GEMM adding
-    // the residual in its epilogue -- the bits of the separate calls.
+    // kernel), the tiles (or their slice sum) forming silu(gate) * up as the
+    // down GEMM's bf16 activations (with Q35MM_GEMM_PAIR=0 the down GEMM
+    // forms it while rounding its activations), the down GEMM adding the
+    // residual in its epilogue -- the bits of the separate calls.
     const q35mm_weight *gu[2] = {gate, up};
     float *gy[2] = {g, u};
     GemmAct act{reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(scr.mlp.ptr) + act_off), false};
