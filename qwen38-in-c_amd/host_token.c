@@ -12,7 +12,8 @@
 #include "q35/q35_mm.h"
 
 typedef struct q35_host_call {
-    uint32_t kind;            /* 0: q35_mm_fp8(W[0]), 1: q35_mm_fp8_multi4(W[0..3]) */
+    uint32_t kind;            /* 0: q35_mm_fp8(W[0]), 1: q35_mm_fp8_multi4(W[0..3]),
+                                 2: q35_mm_fp8_batch(W[0]) over rows[1] tokens */
     uint32_t cols;
     const uint8_t *W[4];
     const uint16_t *sc[4];
@@ -32,6 +33,8 @@ static void run_calls(const q35_host_call *calls, uint32_t n) {
         const q35_host_call *c = &calls[i];
         if (c->kind == 0) {
             q35_mm_fp8(c->W[0], c->sc[0], c->rows[0], c->cols, c->x, c->y[0]);
+        } else if (c->kind == 2) {
+            q35_mm_fp8_batch(c->W[0], c->sc[0], c->rows[0], c->cols, c->rows[1], c->x, c->y[0]);
         } else {
             const uint8_t *W[4] = {c->W[0], c->W[1], c->W[2], c->W[3]};
             const uint16_t *sc[4] = {c->sc[0], c->sc[1], c->sc[2], c->sc[3]};

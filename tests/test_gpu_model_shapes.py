@@ -106,3 +106,18 @@ def test_out_proj_512_tokens_gemm(q, oracle, wl, gpu):
     rel = np.linalg.norm(d) / np.linalg.norm(Yr.astype(np.float64))
     assert rel <= GEMM_REL_L2 and np.abs(d).max() <= GEMM_MAX_ABS, (rel, np.abs(d).max())
     q.release(W)
+
+
+def test_multi4_outputs_beyond_the_direct_path(q, wl, gpu):
+    """A q35_mm_fp8_multi4 whose outputs (400000 + 200000 rows: 2.4 MB) are
+    too large for the kernels to write straight into pinned memory, so they
+    come back over DMA in two chunks, the first ending inside segment 0;
+    each segment the bits of its own q35_mm_fp8 call."""
+    x = wl.gen_act(wl.SEED_BASE + 0x4A, 1, 128)[0]
+    ws = [wl.gen_weight(wl.SEED_BASE + 0x4B + i, n, 128) for i, n in enumerate((400000, 200000))]
+    outs = q.mm_fp8_multi4([W for W, _ in ws], [sc for _, sc in ws], x)
+    for (W, sc), y in zip(ws, outs[:2]):
+        assert (q.mm_fp8(W, sc, x).view(np.uint32) == y.view(np.uint32)).all()
+    for W, _ in ws:
+        q.release(W)
+
