@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -20,6 +21,8 @@
 #include "q35mm/q35mm.h"
 #include "q35mm_internal.h"
 #include "safetensors.h"
+
+#include <unistd.h>
 
 #define Q35MM_API extern "C" __attribute__((visibility("default")))
 
@@ -130,6 +133,7 @@ struct Device {
     uint32_t gemm_min_m = 64;
     bool gemm_narrow = true;    // Q35MM_GEMM_NARROW=0: 256-token tiles for every m
     bool gemm_pair = true;      // Q35MM_GEMM_PAIR=0: two weights of one shape as separate tiles
+    size_t xfer_chunk = 2u << 20;   // Q35MM_XFER_CHUNK_KB: chunk of a large host transfer (0: one piece)
     uint32_t cus = 256;
     uint32_t gemv_per_cu = kGemvCtasPerCu;
     bool trust_pointers = false;
@@ -164,6 +168,7 @@ int ensure_device() {
     g_dev.gemm_min_m = env_u32("Q35MM_GEMM_MIN_M", 64);
     g_dev.gemm_narrow = env_u32("Q35MM_GEMM_NARROW", 1) != 0;
     g_dev.gemm_pair = env_u32("Q35MM_GEMM_PAIR", 1) != 0;
+    g_dev.xfer_chunk = (size_t)env_u32("Q35MM_XFER_CHUNK_KB", 2048) << 10;
     g_dev.trust_pointers = env_u32("Q35MM_TRUST_POINTERS", 0) != 0;
     {
         const char *v = getenv("Q35MM_VERIFY_WEIGHTS");
@@ -1092,14 +1097,82 @@ hipError_t wait_done(hipStream_t st, uint32_t v) {
 // more than the launch latency they would hide.)
 constexpr size_t kDirectBytes = 256 * 1024;
 constexpr int kStale = -1000;   // internal: a resident weight changed behind its pointer
-// Larger transfers run in chunks so that the host's copies and the DMA
-// overlap: chunk i of the activations is copied into pinned memory while
+// Larger transfers run in chunks (Q35MM_XFER_CHUNK_KB, default 2048; at
+// most kXferChunks) so that the host's copies and the DMA overlap: chunk i
+// of the activations is copied into pinned memory while
 // chunk i-1 crosses PCIe, and chunk j of the outputs is copied out of
 // pinned memory while chunk j+1 crosses.  (Each alone runs at ~55 GB/s over
 // PCIe and 32-70 GB/s for the host copy; one after the other they took a
 // 512-token 6144 -> 5120 call 1.21 ms.)
-constexpr size_t kXferChunk = 2u << 20;
 constexpr uint32_t kXferChunks = sizeof(Device::xfer_ev) / sizeof(hipEvent_t);
+
+// Host copies of large transfer chunks, split between the calling thread
+// and one helper thread (a single host thread copies 32-35 GB/s from memory
+// the CPU caches do not hold, below the ~55 GB/s of the DMA it overlaps
+// with).  Calls are serialised by the library lock, so there is one job
+// slot.  The helper is created on first use and never joined (it waits on
+// its condition variable until the process ends; the object is never
+// destroyed, so nothing it uses goes away under it); a process forked
+// after it started copies on its own thread only.
+class CopyHelper {
+  public:
+    void copy(void *dst, const void *src, size_t n) {
+        if (n < kSplitMin || !start()) {
+            memcpy(dst, src, n);
+            return;
+        }
+        const size_t h = (n / 2) & ~(size_t)63;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            dst_ = (uint8_t *)dst + h;
+            src_ = (const uint8_t *)src + h;
+            n_ = n - h;
+            pending_ = true;
+        }
+        cv_.notify_one();
+        memcpy(dst, src, h);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return !pending_; });
+    }
+
+  private:
+    static constexpr size_t kSplitMin = 256u << 10;
+    bool start() {
+        if (started_ && owner_ == getpid()) return true;
+        if (started_) return false;   // forked child: the helper did not come along
+        try {
+            std::thread([this] { run(); }).detach();
+        } catch (...) {
+            return false;
+        }
+        started_ = true;
+        owner_ = getpid();
+        return true;
+    }
+    void run() {
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            cv_.wait(lk, [&] { return pending_; });
+            lk.unlock();
+            memcpy(dst_, src_, n_);
+            lk.lock();
+            pending_ = false;
+            done_cv_.notify_one();
+        }
+    }
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    uint8_t *dst_ = nullptr;
+    const uint8_t *src_ = nullptr;
+    size_t n_ = 0;
+    bool pending_ = false;
+    bool started_ = false;
+    pid_t owner_ = 0;
+};
+CopyHelper &copy_helper() {
+    static CopyHelper *h = new CopyHelper();   // never destroyed: the helper thread outlives static teardown
+    return *h;
+}
 
 // Chunk c of n over 'bytes' (16-byte aligned boundaries).
 inline void xfer_chunk(size_t bytes, uint32_t n, uint32_t c, size_t *off, size_t *len) {
@@ -1108,7 +1181,8 @@ inline void xfer_chunk(size_t bytes, uint32_t n, uint32_t c, size_t *off, size_t
     *len = std::min(bytes, *off + per) - *off;
 }
 inline uint32_t xfer_chunks(size_t bytes) {
-    return (uint32_t)std::min<size_t>(kXferChunks, std::max<size_t>(1, (bytes + kXferChunk - 1) / kXferChunk));
+    const size_t c = g_dev.xfer_chunk;
+    return c ? (uint32_t)std::min<size_t>(kXferChunks, std::max<size_t>(1, (bytes + c - 1) / c)) : 1u;
 }
 
 template <class Run, class Verify>
@@ -1141,7 +1215,7 @@ int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t
         for (uint32_t c = 0; c < nc; c++) {
             size_t o, len;
             xfer_chunk(xb, nc, c, &o, &len);
-            memcpy((uint8_t *)px + o, (const uint8_t *)X + o, len);
+            copy_helper().copy((uint8_t *)px + o, (const uint8_t *)X + o, len);
             e = hipMemcpyAsync((uint8_t *)g_dev.dx.ptr + o, (uint8_t *)px + o, len, hipMemcpyHostToDevice, st);
             if (e != hipSuccess) return fail(set_error(Q35MM_EHIP, "activation copy: %s", hipGetErrorString(e)));
         }
@@ -1197,7 +1271,7 @@ int host_roundtrip(const float *X, size_t xfloats, float *const *Y, const size_t
             size_t seg0 = 0;
             for (uint32_t s = 0; s < nseg; s++) {
                 const size_t sb = yfloats[s] * sizeof(float), a = std::max(o, seg0), b = std::min(o + len, seg0 + sb);
-                if (a < b) memcpy((uint8_t *)Y[s] + (a - seg0), (uint8_t *)py + a, b - a);
+                if (a < b) copy_helper().copy((uint8_t *)Y[s] + (a - seg0), (uint8_t *)py + a, b - a);
                 seg0 += sb;
             }
         }
