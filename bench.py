@@ -121,14 +121,14 @@ def time_graph(torch, fn, steps: int, warmup: int, use_graph: bool):
     return t0.elapsed_time(t1) / 1e3, None
 
 
-def measured_traffic(profile: str):
-    """HBM bytes per launch of the decode GEMV from the committed rocprofv3
-    counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against a copy of
-    known size), or None if that summary is absent."""
+def measured_traffic(profile: str, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch of a line's dominant kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against
+    a copy of known size), or None if that summary is absent."""
     path = os.path.join(ROOT, "profiles", profile)
     try:
         for ln in open(path):
-            if ln.startswith("traffic_bytes_per_launch"):
+            if ln.startswith(key + " "):
                 return int(ln.split()[1])
     except OSError:
         pass
@@ -1014,7 +1014,11 @@ def main():
                            "hip graph" if not args.eager else "eager")},
             "roofline": {"bound": "mfma", "achieved": round(tf_all, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf_all / BF16_PEAK_TFLOPS, 4),
-                         "traffic": None,
+                         "traffic": measured_traffic("gemm_kernels_prefill_m512.md",
+                                                     "prefill_traffic_bytes_per_launch"),
+                         "traffic_source": "profile, not this run: profiles/gemm_kernels_prefill_m512.md "
+                                           "(rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 of the gate+up "
+                                           "GEMM launch, the dominant kernel; factors from a 512 MiB copy)",
                          "kernel": "gemm_fp8_kernel (+ act_to_bf16_kernel, gemm_tail_kernel / "
                                    "gemm_reduce_kernel): whole calls",
                          "flops_per_step": tot_flops,
