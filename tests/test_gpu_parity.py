@@ -364,6 +364,35 @@ def test_gemm_zero_scale_blocks(q, oracle, wl, gpu):
     assert (Y[:, 256:384] == 0).all()
 
 
+@pytest.mark.parametrize("pair", [False, True])
+def test_gemm_whole_rounds_then_k_slices(q, oracle, wl, gpu, pair):
+    """A long prompt (1200 tokens): whole rounds of 256 x 256 tiles, then a
+    last partial round of 24 tiles cut along K, in one launch -- one weight
+    of 14336 rows, or (paired tiles) two of 7168.  Checked on 384 sampled
+    output columns of each weight against the oracle."""
+    import torch
+    m, k = 1200, 1024
+    shapes = [7168, 7168] if pair else [14336]
+    Ws = [wl.gen_weight(0x9C0 + i, n, k) for i, n in enumerate(shapes)]
+    X = wl.gen_act(0x9C8, m, k, bf16=True)
+    ws = [q.Weight(*w) for w in Ws]
+    Ys = [torch.empty((m, n), dtype=torch.float32, device=gpu) for n in shapes]
+    dX = _torch_dev(X, gpu)
+    if pair:
+        q.matmul_multi(ws, dX, Ys)
+    else:
+        q.gemm(ws[0], dX, Ys[0])
+    torch.cuda.synchronize()
+    for i, ((W, sc), Y) in enumerate(zip(Ws, Ys)):
+        n = W.shape[0]
+        idx = np.sort(np.random.default_rng(n + i).choice(n, 384, replace=False)).astype(np.uint32)
+        idx[:2] = [0, n - 1]
+        rel, mx = _gemm_check(Y.cpu().numpy()[:, idx], oracle.mm_rows(W, sc, X, idx))
+        assert rel <= GEMM_REL_L2 and mx <= GEMM_MAX_ABS, (i, rel, mx)
+    for w in ws:
+        w.free()
+
+
 @pytest.mark.parametrize("m", [96, 200])
 def test_gemm_paired_zero_scale_blocks(q, oracle, wl, gpu, m):
     """Paired tiles of two weights whose zero-scale blocks differ (each
