@@ -13,6 +13,10 @@
 - The drop-in entry points called from several host threads at once (the
   reference is called from one thread; the library serialises calls behind
   one lock): every result the bits of the same call made alone.
+- Graphs: calls captured on a stream the library has not seen, replayed
+  with eager calls in between (the GEMM, the MLP block at decode and
+  prefill), every replay the eager bits; scratch that grew after a capture
+  stays alive for the graph; a capture cannot grow scratch.
 
 Bars: decode GEMV ||y - y_ref||_inf / ||y_ref||_inf <= 1e-5; prefill GEMM
 rel-L2 <= 5e-3 and max-abs <= 2e-2; bitwise where results must equal
@@ -227,6 +231,47 @@ def test_graph_captured_on_a_fresh_stream(q, wl, gpu):
         torch.cuda.synchronize()
     del g
     w.free()
+
+
+@pytest.mark.parametrize("m,H,I", [(1, 640, 1664), (200, 640, 1664), (300, 1024, 16640)])
+def test_graph_of_mlp_blocks(q, wl, gpu, m, H, I):
+    """q35mm_mlp captured in a graph on a fresh stream after an eager call:
+    decode (m = 1: the paired GEMV with the RMSNorm inside, then down) and
+    prefill (paired gate+up tiles writing the down GEMM's bf16 activations:
+    64x64 tiles only at 200 tokens, whole tiles, padding tokens and a fused
+    tail at 300).  Each replay, from the same input with eager MLP calls of
+    another size in between, gives the eager bits."""
+    import torch
+    ws = {}
+    for i, nm in enumerate(("gate", "up", "down")):
+        rows, cols = (H, I) if nm == "down" else (I, H)
+        ws[nm] = q.Weight(*wl.gen_weight(0x7A0 + i + I, rows, cols))
+    rng = np.random.default_rng(m)
+    x0 = _dev(rng.standard_normal((m, H)).astype(np.float32), gpu)
+    nw = _dev((rng.standard_normal(H) * 0.1).astype(np.float32), gpu)
+    want = x0.clone()
+    q.mlp(ws["gate"], ws["up"], ws["down"], nw, want)        # eager, warms the stream's workspace
+    torch.cuda.synchronize()
+    X = x0.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            q.mlp(ws["gate"], ws["up"], ws["down"], nw, X)
+    torch.cuda.synchronize()
+    other = _dev(rng.standard_normal((max(1, m // 2), H)).astype(np.float32), gpu)
+    for r in range(3):
+        X.copy_(x0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert (X.cpu().numpy().view(np.uint32) == want.cpu().numpy().view(np.uint32)).all(), r
+        q.mlp(ws["gate"], ws["up"], ws["down"], nw, other)
+        torch.cuda.synchronize()
+    del g
+    for w in ws.values():
+        w.free()
 
 
 def test_graph_replays_after_its_scratch_grew(q, wl, gpu):
