@@ -121,6 +121,23 @@ def time_graph(torch, fn, steps: int, warmup: int, use_graph: bool):
     return t0.elapsed_time(t1) / 1e3, None
 
 
+def clock_peak_tflops(cus: int):
+    """Dense bf16 MFMA peak from this device's peak engine clock (HIP's
+    hipDeviceAttributeClockRate, kHz) and CU count: 4 SIMDs per CU, one
+    32x32x16 MFMA (32768 flop) per 32 cycles per SIMD.  None when the
+    runtime does not say."""
+    import ctypes as C
+    try:
+        hip = C.CDLL("libamdhip64.so")
+        v = C.c_int(0)
+        if hip.hipDeviceGetAttribute(C.byref(v), 5, 0) != 0 or v.value <= 0:   # 5: hipDeviceAttributeClockRate
+            return None
+    except OSError:
+        return None
+    mhz = v.value / 1e3
+    return {"TFLOP/s": round(cus * 4 * 1024 * mhz * 1e6 / 1e12, 1), "clock_MHz": mhz, "CUs": cus}
+
+
 def measured_traffic(profile: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch of a line's dominant kernel from the committed
     rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against
@@ -1022,7 +1039,8 @@ def main():
                          "kernel": "gemm_fp8_kernel (+ act_to_bf16_kernel, gemm_tail_kernel / "
                                    "gemm_reduce_kernel): whole calls",
                          "flops_per_step": tot_flops,
-                         "flops_per_call": {name: wl.flops(512, k, n) for name, k, n in wl.PREFILL_SHAPES}},
+                         "flops_per_call": {name: wl.flops(512, k, n) for name, k, n in wl.PREFILL_SHAPES},
+                         "peak_from_clock": clock_peak_tflops(props.multi_processor_count)},
             "cpu_baseline": None,
             "calls": calls,
             "note": "value = 2*M*N*K of both calls / the time of both whole calls (the fp32->bf16 activation "
