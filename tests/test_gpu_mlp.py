@@ -197,7 +197,7 @@ def test_mlp_block_real_shape(q, oracle, wl, gpu, m):
                                    (1, 8200, 256), (1, 5120, 17408), (64, 640, 1664), (100, 645, 1000),
                                    (1, 645, 1000), (1, 520, 1000), (1, 8192, 272), (200, 645, 1000),
                                    (300, 1032, 640), (300, 256, 16640), (128, 5120, 17408), (512, 5120, 17408),
-                                   (1200, 512, 7168)])
+                                   (1200, 512, 7168), (100, 256, 70000)])
 def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
     """The block entry point gives the bits of the separate device calls it
     stands for (rmsnorm, gate+up, swiglu, down, add), whichever fusion the
@@ -215,7 +215,8 @@ def test_mlp_block_equals_its_steps_bitwise(q, wl, gpu, m, H, I):
     slices of narrow tiles up to 128 tokens, by their slice sum; above: 64x64
     tiles only, whole tiles with padding tokens and a fused 64x64 tail,
     I = 1000 with a partial last K block, and at 1200 tokens whole rounds
-    then a partial round cut along K in one launch); the residual add in the
+    then a partial round cut along K in one launch; at 100 tokens and
+    I = 70000 whole narrow tiles then K slices); the residual add in the
     down GEMM's epilogue."""
     import torch
     _, dw = _mlp_weights(q, wl, H, I, wl.SEED_BASE + 0x320 + H)

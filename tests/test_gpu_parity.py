@@ -316,14 +316,15 @@ def test_gemm_multi_segment(q, oracle, wl, gpu, m):
         w.free()
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 1000, 3000), (200, 1000, 3000), (200, 1000, 1000), (300, 256, 16640)])
+@pytest.mark.parametrize("m,k,n", [(64, 1000, 3000), (200, 1000, 3000), (200, 1000, 1000), (300, 256, 16640),
+                                   (100, 256, 70000)])
 def test_gemm_multi_two_weights_of_one_shape(q, oracle, wl, gpu, m, k, n):
     """Two weights of one shape (the MLP's gate and up) on the GEMM path run
     as paired tiles, each holding the same rows of both weights: narrow tiles
     cut along K (64 tokens), 256 x 256 tiles cut along K (200 x 3000), only
     64x64 tiles (200 x 1000), whole tiles with padding tokens and a fused
-    64x64 tail (300 x 16640).  Each output within the GEMM bars of the
-    oracle."""
+    64x64 tail (300 x 16640), whole narrow tiles then a round cut along K
+    (100 x 70000).  Each output within the GEMM bars of the oracle."""
     import torch
     Ws = [wl.gen_weight(0x9A1 + i + n, n, k) for i in range(2)]
     X = wl.gen_act(0x9A3 + m, m, k)
